@@ -1,0 +1,83 @@
+// Device-side helpers shared by the MoE kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jgmoe {
+
+constexpr int kBlock = 128;     // scale-block edge (1x128 activations, 128x128 weights)
+constexpr int kWave = 64;
+constexpr int kMaxTopK = 8;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
+  return __uint_as_float((uint32_t)b << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (inputs here are finite).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Monotone map of a finite float onto uint32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t float_order_key(float v) {
+  uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// One v_mfma_f32_16x16x128_f8f6f4 (both operands OCP e4m3), fresh accumulator.
+// Operand layout (verified on gfx950): lane l supplies row/column (l & 15) and the 32 K-values
+// [32*(l>>4), 32*(l>>4)+32) of the 128-wide K block; result lane l holds D[4*(l>>4)+i][l & 15].
+__device__ __forceinline__ v4f mfma_f8_16x16x128(const v8i& a, const v8i& b) {
+  v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x32_bf16: lane l supplies row/column (l & 15), K-values [8*(l>>4), +8).
+__device__ __forceinline__ v4f mfma_bf16_16x16x32(const v8bf& a, const v8bf& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Four e4m3 bytes -> four bf16 (exact: every e4m3 value is representable in bf16).
+__device__ __forceinline__ void fp8x4_to_bf16x4(int packed, v2bf& lo, v2bf& hi) {
+  lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(packed, 1.0f, false);
+  hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(packed, 1.0f, true);
+}
+
+// Maps a linear M-tile slot onto (local expert, first row within its segment) from the
+// per-expert pair counts: each expert owns ceil(count / bm) consecutive slots. Every lane of
+// the wave must call it; the result is wave-uniform. Returns false for slots past the end.
+__device__ __forceinline__ bool find_m_tile(const int32_t* __restrict__ counts, int n_experts,
+                                            int bm, int slot, int& expert, int& m0) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int base = 0;
+  for (int c0 = 0; c0 < n_experts; c0 += kWave) {
+    const int ex = c0 + lane;
+    const int n = ex < n_experts ? (counts[ex] + bm - 1) / bm : 0;
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      int y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
+    }
+    const int excl = incl - n;
+    const bool hit = slot >= base + excl && slot < base + incl;
+    const unsigned long long m = __ballot(hit);
+    if (m) {
+      const int src = __ffsll((long long)m) - 1;
+      expert = c0 + src;
+      m0 = (slot - base - __shfl(excl, src)) * bm;
+      return true;
+    }
+    base += __shfl(incl, kWave - 1);
+  }
+  return false;
+}
+
+}  // namespace jgmoe

@@ -1,0 +1,38 @@
+// Host-side launchers of the MoE kernels (internal to the library; the public ABI is
+// include/justgoal_moe.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jgmoe {
+
+constexpr int ROUTING_DS = 0;
+constexpr int ROUTING_SOFTMAX = 1;
+
+hipError_t launch_route(const float* logits, const uint16_t* bias, int T, int E, int n_group,
+                        int topk_group, int top_k, int method, float rsf, int32_t* topk_idx,
+                        float* topk_w, hipStream_t stream);
+
+hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, int T, int K,
+                          int local_offset, int E_l, int32_t* counts, int32_t* offsets,
+                          int32_t* sorted_tok, float* sorted_w, int32_t* pair_of,
+                          hipStream_t stream);
+
+// Grouped GEMM1 (W13) with the SwiGLU epilogue: C[p, :] = bf16(X1 * silu(X2)) for every pair p.
+// max_pairs bounds the number of pairs (sizes the grid; surplus workgroups exit at once);
+// rows_hint, the expected pairs per expert under uniform routing, picks the tile shape.
+hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
+                        const float* s13, const int32_t* counts, const int32_t* offsets,
+                        const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
+                        int max_pairs, int rows_hint, hipStream_t stream);
+
+// Grouped GEMM2 (W2): partial[p, :] = w_p * (C[p, :] @ W2[e]^T) in fp32.
+hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
+                        const int32_t* counts, const int32_t* offsets, const float* sorted_w,
+                        float* partial, int H, int I, int E_l, int max_pairs, int rows_hint, hipStream_t stream);
+
+// out[t, :] = bf16(sum of partial rows of t's local pairs, ascending local expert), 0 if none.
+hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,
+                          uint16_t* out, hipStream_t stream);
+
+}  // namespace jgmoe

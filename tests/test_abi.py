@@ -1,0 +1,80 @@
+"""The C ABI library: it loads, exports every symbol the public header declares, and its host-side
+validation answers without touching a GPU (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from justgoal_amd import _lib
+from justgoal_amd.geometry import DS_V3, QWEN3, ROUTING_DS, Geometry
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "justgoal_moe.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(moe_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_binding_list():
+    assert declared_functions() == sorted(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_workspace_bytes_matches_layout():
+    L = _lib.lib()
+    for T in (0, 1, 64, 16384):
+        n = L.moe_workspace_bytes(T)
+        assert n == _lib.workspace_layout(DS_V3, T)["total"]
+    # 16384 tokens need more than INT_MAX bytes: the int64 return carries it
+    assert L.moe_workspace_bytes(16384) > 2**31
+
+
+def test_layout_regions_ordered_and_aligned():
+    lay = _lib.workspace_layout(QWEN3, 1000)
+    offs = [lay[n] for n in _lib.WS_REGIONS] + [lay["total"]]
+    assert offs == sorted(offs)
+    assert all(o % 256 == 0 for o in offs)
+    # C region holds Np x I bf16
+    Np = 1000 * 8
+    assert lay["partial"] - lay["C"] >= Np * QWEN3.intermediate * 2
+
+
+@pytest.mark.parametrize("bad", [
+    Geometry(7100, 2048, 256, 32, 8, 8, 4, ROUTING_DS),    # H not a multiple of 128
+    Geometry(7168, 2000, 256, 32, 8, 8, 4, ROUTING_DS),    # I not a multiple of 128
+    Geometry(7168, 2048, 200, 32, 8, 8, 4, ROUTING_DS),    # E not a multiple of 64
+    Geometry(7168, 2048, 256, 32, 9, 8, 4, ROUTING_DS),    # top_k > 8
+    Geometry(7168, 2048, 256, 32, 8, 3, 2, ROUTING_DS),    # groups do not divide E
+    Geometry(7168, 2048, 256, 32, 8, 8, 9, ROUTING_DS),    # topk_group > n_group
+    Geometry(7168, 2048, 256, 32, 8, 8, 4, 7),             # unknown routing method
+])
+def test_bad_geometry_rejected(bad):
+    L = _lib.lib()
+    g = bad.c_struct()
+    assert L.moe_workspace_bytes_ex(ctypes.byref(g), 16) == -2
+    rc = L.moe_run_ex(ctypes.byref(g), *([1] * 8), 0, 1.0, 1, 1, 16, None)
+    assert rc == -2
+    assert "geometry" in L.moe_error_string(rc).decode()
+
+
+def test_null_pointers_and_negative_T_rejected_on_host():
+    L = _lib.lib()
+    args = [1] * 8
+    assert L.moe_run(*args, 0, 2.5, 1, 1, -1, None) == -1
+    assert L.moe_run(None, *args[1:], 0, 2.5, 1, 1, 16, None) == -1
+    assert L.moe_run(*args, 0, 2.5, None, 1, 16, None) == -1
+    assert L.moe_run(*args, 0, 2.5, 1, None, 16, None) == -1
+
+
+def test_zero_tokens_is_a_no_op():
+    # T = 0: nothing to enqueue, success without a device
+    assert _lib.lib().moe_run(*([None] * 8), 0, 2.5, None, None, 0, None) == 0

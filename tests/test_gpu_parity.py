@@ -1,0 +1,194 @@
+"""GPU parity: the HIP operator (through the C ABI) against the CPU oracle.
+
+Bars: routing indices, weights, segment layout and pair map bit-exact; bf16 output within
+rtol = atol = 2e-2 of the oracle's dequantise-then-fp32 result. Full-size configurations that the
+CPU oracle cannot finish in seconds are checked on a token sample (each token's output depends
+only on its own row, so a sampled row is checked exactly as in a full run) plus size-independent
+properties (segment invariants, determinism).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from justgoal_amd import inputs as jin
+from justgoal_amd.geometry import DS_V3, QWEN3, ROUTING_DS, ROUTING_SOFTMAX, Geometry
+from justgoal_amd.moe import run, workspace, workspace_views
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 2e-2
+ATOL = 2e-2
+
+MINI_DS = Geometry(512, 256, 256, 32, 8, 8, 4, ROUTING_DS, "mini-DS")
+MINI_SOFTMAX = Geometry(256, 384, 128, 128, 8, 1, 1, ROUTING_SOFTMAX, "mini-softmax")
+SMALL_GROUPS = Geometry(256, 128, 64, 16, 4, 4, 2, ROUTING_DS, "small-groups")
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+_WEIGHTS = {}
+
+
+def weights_for(geom, device):
+    key = (geom, str(device))
+    if key not in _WEIGHTS:
+        w = jin.make_weights(geom, seed=1)
+        _WEIGHTS[key] = (w, tuple(t.to(device) for t in w))
+    return _WEIGHTS[key]
+
+
+def to_dev(d, device):
+    return {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+def subset_tokens(inp_cpu, tok):
+    """The operator's inputs restricted to a token subset (routing and output are per-token)."""
+    t = torch.as_tensor(tok, dtype=torch.long)
+    d = dict(inp_cpu)
+    d["routing_logits"] = inp_cpu["routing_logits"][t]
+    d["hidden_states"] = inp_cpu["hidden_states"][t]
+    d["hidden_states_scale"] = inp_cpu["hidden_states_scale"][:, t].contiguous()
+    return d
+
+
+def check_case(geom, T, device, seed=0, tokens_checked=None, local_offset=0, bias=True,
+               skew=(0, 0.0), rsf=None):
+    (w_cpu, w_dev) = weights_for(geom, device)
+    act = jin.make_activations(geom, T, seed=seed, skew_experts=skew[0], skew_offset=skew[1],
+                               local_offset=local_offset)
+    if not bias:
+        act["routing_bias"] = None
+    inp_cpu = dict(act, gemm1_weights=w_cpu[0], gemm1_weights_scale=w_cpu[1],
+                   gemm2_weights=w_cpu[2], gemm2_weights_scale=w_cpu[3],
+                   local_expert_offset=local_offset,
+                   routed_scaling_factor=(rsf if rsf is not None else
+                                          (2.5 if geom.routing_method == ROUTING_DS else 1.0)))
+    inp_dev = dict(to_dev(act, device), gemm1_weights=w_dev[0], gemm1_weights_scale=w_dev[1],
+                   gemm2_weights=w_dev[2], gemm2_weights_scale=w_dev[3],
+                   local_expert_offset=local_offset,
+                   routed_scaling_factor=inp_cpu["routed_scaling_factor"])
+    say(f"[case] geom={geom.name} T={T} seed={seed} off={local_offset} bias={bias} skew={skew}")
+    out = run(**inp_dev, geometry=geom)
+    torch.cuda.synchronize()
+    ws = workspace_views(geom, T, workspace(geom, T, device))
+
+    # routing + permute: bit-exact against the oracle over all T tokens
+    idx, w = oracle.route(inp_cpu["routing_logits"], inp_cpu["routing_bias"], geom,
+                          inp_cpu["routed_scaling_factor"])
+    np.testing.assert_array_equal(ws["topk_idx"].cpu().numpy(), idx)
+    np.testing.assert_array_equal(ws["topk_w"].cpu().numpy().view(np.uint32), w.view(np.uint32))
+    perm = oracle.permute(idx, w, local_offset, geom.local_experts)
+    np.testing.assert_array_equal(ws["counts"].cpu().numpy(), perm["counts"])
+    np.testing.assert_array_equal(ws["offsets"].cpu().numpy(), perm["offsets"])
+    n = int(perm["offsets"][-1])
+    np.testing.assert_array_equal(ws["sorted_tok"][:n].cpu().numpy(), perm["sorted_tok"])
+    np.testing.assert_array_equal(ws["sorted_w"][:n].cpu().numpy().view(np.uint32),
+                                  perm["sorted_w"].view(np.uint32))
+    np.testing.assert_array_equal(ws["pair_of"].cpu().numpy(), perm["pair_of"])
+
+    # output
+    if tokens_checked is None:
+        tok = np.arange(T)
+        ref = oracle.moe_reference(inp_cpu, geom)
+    else:
+        rng = np.random.default_rng(seed)
+        tok = np.sort(rng.choice(T, size=min(T, tokens_checked), replace=False))
+        ref = oracle.moe_reference(subset_tokens(inp_cpu, tok), geom)
+    got = out.cpu()[torch.as_tensor(tok)]
+    err = (got.float() - ref.float()).abs()
+    tol = ATOL + RTOL * ref.float().abs()
+    bad = int((err > tol).sum())
+    say(f"  pairs={n} max_abs_err={float(err.max()):.3e} n_bad={bad} of {err.numel()}")
+    torch.testing.assert_close(got.float(), ref.float(), rtol=RTOL, atol=ATOL)
+    return out, ws
+
+
+@pytest.mark.parametrize("T", [1, 5, 16, 64, 300, 1000])
+def test_mini_ds(gpu, T):
+    check_case(MINI_DS, T, gpu, seed=T)
+
+
+@pytest.mark.parametrize("T", [1, 37, 700])
+def test_mini_softmax(gpu, T):
+    check_case(MINI_SOFTMAX, T, gpu, seed=T)
+
+
+@pytest.mark.parametrize("T", [3, 200])
+def test_small_groups(gpu, T):
+    check_case(SMALL_GROUPS, T, gpu, seed=T)
+
+
+@pytest.mark.parametrize("off", [32, 224, 256])
+def test_local_offset(gpu, off):
+    # 224: the last EP rank; 256: no expert is local, the output must be all zeros
+    out, ws = check_case(MINI_DS, 40, gpu, seed=off, local_offset=off)
+    if off == 256:
+        assert int(ws["offsets"][-1]) == 0
+        assert torch.count_nonzero(out).item() == 0
+
+
+def test_no_bias(gpu):
+    check_case(MINI_DS, 50, gpu, seed=7, bias=False)
+
+
+def test_t_zero(gpu):
+    act = jin.make_activations(MINI_DS, 0)
+    w = weights_for(MINI_DS, gpu)[1]
+    out = run(**to_dev(act, gpu), gemm1_weights=w[0], gemm1_weights_scale=w[1],
+              gemm2_weights=w[2], gemm2_weights_scale=w[3], local_expert_offset=0,
+              routed_scaling_factor=2.5, geometry=MINI_DS)
+    assert out.shape == (0, MINI_DS.hidden)
+
+
+def test_ds_config0_t16(gpu):
+    check_case(DS_V3, 16, gpu, seed=0)
+
+
+def test_ds_config1_t64(gpu):
+    check_case(DS_V3, 64, gpu, seed=0)
+
+
+def test_ds_config2_t4096(gpu):
+    check_case(DS_V3, 4096, gpu, seed=0, tokens_checked=256)
+
+
+def test_ds_config3_t16384_skew(gpu):
+    out, ws = check_case(DS_V3, 16384, gpu, seed=0, tokens_checked=96, skew=(8, 3.0))
+    c = ws["counts"].cpu().numpy()
+    assert c[:8].sum() > 0.5 * c.sum()   # the boosted experts take most of the local pairs
+
+
+def test_qwen3_config4_t1024(gpu):
+    check_case(QWEN3, 1024, gpu, seed=0, tokens_checked=256)
+
+
+def test_deterministic(gpu):
+    """Two calls on the same inputs give bit-identical outputs (no atomics anywhere)."""
+    w = weights_for(MINI_DS, gpu)[1]
+    act = to_dev(jin.make_activations(MINI_DS, 777, seed=3), gpu)
+    kw = dict(act, gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2],
+              gemm2_weights_scale=w[3], local_expert_offset=0, routed_scaling_factor=2.5,
+              geometry=MINI_DS)
+    a = run(**kw).clone()
+    b = run(**kw)
+    assert torch.equal(a, b)
+
+
+def test_dps_output(gpu):
+    """Destination-passing form writes into the caller's tensor."""
+    w = weights_for(MINI_DS, gpu)[1]
+    act = to_dev(jin.make_activations(MINI_DS, 33, seed=4), gpu)
+    kw = dict(act, gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2],
+              gemm2_weights_scale=w[3], local_expert_offset=torch.tensor(0),
+              routed_scaling_factor=torch.tensor(2.5))
+    ref = run(**kw, geometry=MINI_DS).clone()
+    dst = torch.full((33, MINI_DS.hidden), float("nan"), dtype=torch.bfloat16, device=gpu)
+    res = run(**kw, output=dst, geometry=MINI_DS)
+    assert res.data_ptr() == dst.data_ptr()
+    assert torch.equal(dst, ref)
