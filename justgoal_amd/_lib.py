@@ -11,7 +11,7 @@ import os
 from .geometry import MoeGeometryC
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libjustgoal_moe.so")
+LIB_PATH = os.environ.get("JUSTGOAL_MOE_LIB") or os.path.join(_HERE, "libjustgoal_moe.so")
 
 # Every symbol include/justgoal_moe.h declares.
 EXPORTED = ("moe_run", "moe_workspace_bytes", "moe_run_ex", "moe_workspace_bytes_ex",

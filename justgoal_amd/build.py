@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libjustgoal_moe.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["moe_api.hip", "moe_routing.hip", "moe_gemm.hip"]
+SOURCES = ["moe_api.hip", "moe_routing.hip", "moe_gemm.hip", "moe_stream.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -26,19 +26,22 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source into one shared library; returns its path."""
+def build(verbose: bool = False, out: str = LIB_PATH, defines=()) -> str:
+    """Compile every source into one shared library; returns its path.
+
+    ``defines`` (e.g. ``["JG_G1_STREAM_D=6"]``) override the kernels' compile-time tuning knobs;
+    the default build uses none."""
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB_PATH + f".{os.getpid()}.tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, *srcs]
+    tmp = out + f".{os.getpid()}.tmp"
+    cmd = [HIPCC, *FLAGS, *[f"-D{d}" for d in defines], "-o", tmp, *srcs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed ({res.returncode}) building {LIB_NAME}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

@@ -24,7 +24,8 @@ bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 // whole lanes in power-of-two lane counts, at most 8 selections.
 int check_geometry(const moe_geometry* g) {
   if (!g) return MOE_ERR_INVALID_ARG;
-  if (g->hidden <= 0 || g->hidden % 128 || g->intermediate <= 0 || g->intermediate % 128)
+  if (g->hidden <= 0 || g->hidden % 128 || g->hidden > 16384 || g->intermediate <= 0 ||
+      g->intermediate % 128)
     return MOE_ERR_GEOMETRY;
   const int E = g->num_experts;
   if (E <= 0 || E % 64 || E > 512 || !is_pow2(E / 64)) return MOE_ERR_GEOMETRY;

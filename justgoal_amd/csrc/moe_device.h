@@ -31,6 +31,35 @@ __device__ __forceinline__ uint32_t float_order_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Load of a T at a wave-uniform base plus a 32-bit per-lane byte offset (lets the compiler use
+// the SGPR-base addressing form, one VGPR per address).
+template <class T>
+__device__ __forceinline__ T ldg(const void* base, uint32_t off) {
+  return *(const T*)((const char*)base + off);
+}
+
+// Raw buffer resource over [base, base + bytes): loads take a per-lane 32-bit VGPR offset plus
+// a wave-uniform SGPR offset, and anything past `bytes` reads as zero instead of faulting.
+// 0x00020000 is the gfx9-family word-3 value for untyped raw access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                            uint32_t soff) {
+  typedef int v4i_ __attribute__((ext_vector_type(4)));
+  const v4i_ v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+}
+
+__device__ __forceinline__ v8i buf_load32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  typedef int v4i_ __attribute__((ext_vector_type(4)));
+  const v4i_ lo = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  const v4i_ hi = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // One v_mfma_f32_16x16x128_f8f6f4 (both operands OCP e4m3), fresh accumulator.
 // Operand layout (verified on gfx950): lane l supplies row/column (l & 15) and the 32 K-values
 // [32*(l>>4), 32*(l>>4)+32) of the 128-wide K block; result lane l holds D[4*(l>>4)+i][l & 15].
@@ -78,6 +107,70 @@ __device__ __forceinline__ bool find_m_tile(const int32_t* __restrict__ counts, 
     base += __shfl(incl, kWave - 1);
   }
   return false;
+}
+
+// Register-resident M-tile map for persistent kernels: lane l keeps expert l + 64*j (j < 4,
+// so up to 256 local experts) with its pair count, segment offset and the inclusive prefix of
+// tile counts. Built once per wave; each lookup is a ballot plus scalar lane reads.
+struct TileMap {
+  int incl[4], ntile[4], cnt[4], seg[4];
+  int total;
+
+  __device__ __forceinline__ void init(const int32_t* __restrict__ counts,
+                                       const int32_t* __restrict__ offsets, int n_experts,
+                                       int bm) {
+    const int lane = threadIdx.x & (kWave - 1);
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = j * kWave + lane;
+      const bool ok = ex < n_experts;
+      cnt[j] = ok ? counts[ex] : 0;
+      seg[j] = ok ? offsets[ex] : 0;
+      ntile[j] = (cnt[j] + bm - 1) / bm;
+      int x = ntile[j];
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+      }
+      incl[j] = base + x;
+      base += __shfl(x, kWave - 1);
+    }
+    total = base;
+  }
+
+  // slot < total. Returns the local expert; m0 = first row of the tile within the segment.
+  __device__ __forceinline__ int find(int slot, int bm, int& m0, int& count, int& segment) const {
+    const int lane = threadIdx.x & (kWave - 1);
+    int e = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned long long m = __ballot(slot < incl[j] && slot >= incl[j] - ntile[j]);
+      if (m) {
+        const int src = __ffsll((long long)m) - 1;
+        const int excl = __builtin_amdgcn_readlane(incl[j] - ntile[j], src);
+        m0 = (slot - excl) * bm;
+        count = __builtin_amdgcn_readlane(cnt[j], src);
+        segment = __builtin_amdgcn_readlane(seg[j], src);
+        e = j * kWave + src;
+        break;
+      }
+    }
+    (void)lane;
+    return e;
+  }
+};
+
+// Total M-tiles over all experts: sum of ceil(count / bm). Wave-uniform; every lane must call.
+__device__ __forceinline__ int count_m_tiles(const int32_t* __restrict__ counts, int n_experts,
+                                             int bm) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int n = 0;
+  for (int ex = lane; ex < n_experts; ex += kWave) n += (counts[ex] + bm - 1) / bm;
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) n += __shfl_xor(n, off);
+  return n;
 }
 
 }  // namespace jgmoe

@@ -278,6 +278,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   *(uint4*)(out + (size_t)t * H + c) = o;
 }
 
+#ifndef JG_STREAM_MAX_ROWS
+#define JG_STREAM_MAX_ROWS 16
+#endif
+
+// M sub-tiles (of 16 rows) per streaming item for an expected segment length.
+static inline int stream_mt(int rows_hint) { return rows_hint <= 16 ? 1 : rows_hint <= 32 ? 2 : 4; }
+
 static inline int m_slots(int max_pairs, int bm, int E_l) {
   return (max_pairs + bm - 1) / bm + (E_l < max_pairs ? E_l : max_pairs);
 }
@@ -287,11 +294,9 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t*
                         const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                         int max_pairs, int rows_hint, hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= 16) {
-    constexpr int MT = 1, NW = 1;
-    const dim3 grid(m_slots(max_pairs, 16 * MT, E_l), I / (64 * NW));
-    gemm1_swiglu_kernel<MT, NW><<<grid, 256, 0, stream>>>(hs, hs_scale, w13, s13, counts,
-                                                          offsets, sorted_tok, C, T, H, I, E_l);
+  if (rows_hint <= JG_STREAM_MAX_ROWS) {
+    return launch_gemm1_stream(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I,
+                               E_l, max_pairs, stream_mt(rows_hint), stream);
   } else {
     constexpr int MT = 4, NW = 2;
     const dim3 grid(m_slots(max_pairs, 16 * MT, E_l), I / (64 * NW));
@@ -305,11 +310,9 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
                         const int32_t* counts, const int32_t* offsets, const float* sorted_w,
                         float* partial, int H, int I, int E_l, int max_pairs, int rows_hint, hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= 16) {
-    constexpr int MT = 1, NW = 2;
-    const dim3 grid(m_slots(max_pairs, 16 * MT, E_l), H / (64 * NW));
-    gemm2_kernel<MT, NW><<<grid, 256, 0, stream>>>(C, w2, s2, counts, offsets, sorted_w, partial,
-                                                   H, I, E_l);
+  if (rows_hint <= JG_STREAM_MAX_ROWS) {
+    return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
+                               max_pairs, stream_mt(rows_hint), stream);
   } else {
     constexpr int MT = 4, NW = 2;
     const dim3 grid(m_slots(max_pairs, 16 * MT, E_l), H / (64 * NW));
