@@ -14,6 +14,13 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
+// Wave index within the workgroup, as a wave-uniform (SGPR) value. Deriving it with a plain
+// division leaves it in a VGPR as far as the compiler knows, and any buffer-load SGPR offset
+// built from it then turns into a per-lane waterfall loop.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+}
+
 __device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
   return __uint_as_float((uint32_t)b << 16);
 }
@@ -59,6 +66,23 @@ __device__ __forceinline__ v8i buf_load32(__amdgpu_buffer_rsrc_t r, uint32_t vof
   const v4i_ hi = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
+
+// A row of up to 128 per-K-block scales held one per lane in two VGPRs. A K loop reads scale
+// kb with a lane read (v_readlane) instead of a scalar memory load: scalar loads complete out of
+// order and share their wait counter with LDS traffic, so consuming a prefetched one would wait
+// for every outstanding scalar load and LDS access.
+struct LaneScales {
+  float v0, v1;
+  __device__ __forceinline__ void load(const float* __restrict__ p, int n) {
+    const int lane = threadIdx.x & (kWave - 1);
+    v0 = lane < n ? p[lane] : 0.f;
+    v1 = lane + kWave < n ? p[lane + kWave] : 0.f;
+  }
+  __device__ __forceinline__ float get(int kb) const {
+    const float v = kb < kWave ? v0 : v1;
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), kb & (kWave - 1)));
+  }
+};
 
 // One v_mfma_f32_16x16x128_f8f6f4 (both operands OCP e4m3), fresh accumulator.
 // Operand layout (verified on gfx950): lane l supplies row/column (l & 15) and the 32 K-values
@@ -107,6 +131,17 @@ __device__ __forceinline__ bool find_m_tile(const int32_t* __restrict__ counts, 
     base += __shfl(incl, kWave - 1);
   }
   return false;
+}
+
+// Workers actually used by a persistent loop over `items` equal work items with `workers`
+// launched: the fewest workers that still need the same number of rounds, so every used worker
+// gets the same number of items and no round runs nearly empty (workers at or past the
+// returned stride do nothing). Computed on the device from the routed counts, which the host
+// never sees.
+__device__ __forceinline__ int balanced_stride(int items, int workers) {
+  if (items <= 0) return workers;
+  const int rounds = (items + workers - 1) / workers;
+  return (items + rounds - 1) / rounds;
 }
 
 // Register-resident M-tile map for persistent kernels: lane l keeps expert l + 64*j (j < 4,

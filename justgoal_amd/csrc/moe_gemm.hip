@@ -24,222 +24,6 @@
 
 namespace jgmoe {
 
-template <int MT, int NW>
-struct G1Stage {
-  v8i a[MT];
-  v8i b1[NW], b2[NW];
-  float sa[MT][4];
-  float sw1, sw2;
-};
-
-template <int MT, int NW>
-__global__ __launch_bounds__(256) void gemm1_swiglu_kernel(
-    const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
-    const uint8_t* __restrict__ w13, const float* __restrict__ s13,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ sorted_tok, uint16_t* __restrict__ C, int T, int H, int I,
-    int E_l) {
-  constexpr int BM = 16 * MT;
-  int e, m0;
-  if (!find_m_tile(counts, E_l, BM, blockIdx.x, e, m0)) return;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int r16 = lane & 15, g = lane >> 4;
-  const int cnt = counts[e], seg = offsets[e];
-  const int c0 = blockIdx.y * (64 * NW) + wave * (16 * NW);
-  const int NKB = H / kBlock;
-
-  const uint8_t* arow[MT];
-  bool aval[MT];
-  int etok[MT][4];
-  bool evalid[MT][4];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = m0 + mt * 16 + r16;
-    aval[mt] = r < cnt;
-    const int tok = aval[mt] ? sorted_tok[seg + r] : 0;
-    arow[mt] = hs + (size_t)tok * H + 32 * g;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int re = m0 + mt * 16 + 4 * g + i;
-      evalid[mt][i] = re < cnt;
-      etok[mt][i] = evalid[mt][i] ? sorted_tok[seg + re] : 0;
-    }
-  }
-  const uint8_t* wrow1 = w13 + ((size_t)e * 2 * I + c0 + r16) * H + 32 * g;
-  const size_t half = (size_t)I * H;
-  const float* sc1 = s13 + ((size_t)e * (2 * I / kBlock) + c0 / kBlock) * NKB;
-  const float* sc2 = s13 + ((size_t)e * (2 * I / kBlock) + (I + c0) / kBlock) * NKB;
-
-  v4f acc1[MT][NW], acc2[MT][NW];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      acc1[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
-      acc2[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    }
-
-  auto load = [&](int kb, G1Stage<MT, NW>& st) {
-    const v8i zero = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      st.a[mt] = aval[mt] ? *(const v8i*)(arow[mt] + kb * kBlock) : zero;
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      const uint8_t* p = wrow1 + (size_t)j * 16 * H + kb * kBlock;
-      st.b1[j] = *(const v8i*)p;
-      st.b2[j] = *(const v8i*)(p + half);
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        st.sa[mt][i] = evalid[mt][i] ? hs_scale[(size_t)kb * T + etok[mt][i]] : 0.f;
-    st.sw1 = sc1[kb];
-    st.sw2 = sc2[kb];
-  };
-  auto compute = [&](const G1Stage<MT, NW>& st) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float f1[4], f2[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f1[i] = st.sa[mt][i] * st.sw1;
-        f2[i] = st.sa[mt][i] * st.sw2;
-      }
-#pragma unroll
-      for (int j = 0; j < NW; ++j) {
-        const v4f p = mfma_f8_16x16x128(st.a[mt], st.b1[j]);
-        const v4f q = mfma_f8_16x16x128(st.a[mt], st.b2[j]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc1[mt][j][i] = fmaf(p[i], f1[i], acc1[mt][j][i]);
-          acc2[mt][j][i] = fmaf(q[i], f2[i], acc2[mt][j][i]);
-        }
-      }
-    }
-  };
-
-  G1Stage<MT, NW> s0, s1;
-  load(0, s0);
-  for (int kb = 0; kb < NKB; kb += 2) {
-    if (kb + 1 < NKB) load(kb + 1, s1);
-    compute(s0);
-    if (kb + 2 < NKB) load(kb + 2, s0);
-    if (kb + 1 < NKB) compute(s1);
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m0 + mt * 16 + 4 * g + i;
-      if (r >= cnt) continue;
-      uint16_t* crow = C + (size_t)(seg + r) * I + c0 + r16;
-#pragma unroll
-      for (int j = 0; j < NW; ++j) {
-        const float x1 = acc1[mt][j][i], x2 = acc2[mt][j][i];
-        crow[16 * j] = float_to_bf16_bits(x1 * (x2 / (1.0f + __expf(-x2))));
-      }
-    }
-}
-
-template <int MT, int NW>
-struct G2Stage {
-  uint4 a[MT][4];
-  v8i b[NW];
-  float sw;
-};
-
-__device__ __forceinline__ v8bf as_v8bf(const uint4& u) { return __builtin_bit_cast(v8bf, u); }
-
-template <int MT, int NW>
-__global__ __launch_bounds__(256) void gemm2_kernel(
-    const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const float* __restrict__ sorted_w, float* __restrict__ partial, int H, int I, int E_l) {
-  constexpr int BM = 16 * MT;
-  int e, m0;
-  if (!find_m_tile(counts, E_l, BM, blockIdx.x, e, m0)) return;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int r16 = lane & 15, g = lane >> 4;
-  const int cnt = counts[e], seg = offsets[e];
-  const int h0 = blockIdx.y * (64 * NW) + wave * (16 * NW);
-  const int NKB = I / kBlock;
-
-  const uint16_t* crow[MT];
-  bool aval[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = m0 + mt * 16 + r16;
-    aval[mt] = r < cnt;
-    crow[mt] = C + (size_t)(seg + (aval[mt] ? r : 0)) * I + 32 * g;
-  }
-  const uint8_t* wrow = w2 + ((size_t)e * H + h0 + r16) * I + 32 * g;
-  const float* sc = s2 + ((size_t)e * (H / kBlock) + h0 / kBlock) * NKB;
-
-  v4f acc[MT][NW];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < NW; ++j) acc[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  auto load = [&](int kb, G2Stage<MT, NW>& st) {
-    const uint4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        st.a[mt][c] = aval[mt] ? *(const uint4*)(crow[mt] + kb * kBlock + 8 * c) : zero;
-#pragma unroll
-    for (int j = 0; j < NW; ++j) st.b[j] = *(const v8i*)(wrow + (size_t)j * 16 * I + kb * kBlock);
-    st.sw = sc[kb];
-  };
-  auto compute = [&](const G2Stage<MT, NW>& st) {
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      v8bf bc[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        v2bf p0, p1, p2, p3;
-        fp8x4_to_bf16x4(st.b[j][2 * c], p0, p1);
-        fp8x4_to_bf16x4(st.b[j][2 * c + 1], p2, p3);
-        bc[c] = v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        v4f t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) t = mfma_bf16_16x16x32(as_v8bf(st.a[mt][c]), bc[c], t);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(t[i], st.sw, acc[mt][j][i]);
-      }
-    }
-  };
-
-  G2Stage<MT, NW> s0, s1;
-  load(0, s0);
-  for (int kb = 0; kb < NKB; kb += 2) {
-    if (kb + 1 < NKB) load(kb + 1, s1);
-    compute(s0);
-    if (kb + 2 < NKB) load(kb + 2, s0);
-    if (kb + 1 < NKB) compute(s1);
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = m0 + mt * 16 + 4 * g + i;
-      if (r >= cnt) continue;
-      const int p = seg + r;
-      const float wp = sorted_w[p];
-      float* orow = partial + (size_t)p * H + h0 + r16;
-#pragma unroll
-      for (int j = 0; j < NW; ++j) orow[16 * j] = acc[mt][j][i] * wp;
-    }
-}
-
 // One thread per (token, 8 consecutive hidden columns).
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
                                                       const int32_t* __restrict__ pair_of, int T,
@@ -282,44 +66,36 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 #define JG_STREAM_MAX_ROWS 16
 #endif
 
-// M sub-tiles (of 16 rows) per streaming item for an expected segment length.
-static inline int stream_mt(int rows_hint) { return rows_hint <= 16 ? 1 : rows_hint <= 32 ? 2 : 4; }
+#ifndef JG_TILE_MT8_ROWS
+#define JG_TILE_MT8_ROWS 256
+#endif
 
-static inline int m_slots(int max_pairs, int bm, int E_l) {
-  return (max_pairs + bm - 1) / bm + (E_l < max_pairs ? E_l : max_pairs);
-}
+// M sub-tiles (of 16 rows) per work item for an expected segment length.
+static inline int stream_mt(int rows_hint) { return rows_hint <= 16 ? 1 : rows_hint <= 32 ? 2 : 4; }
+static inline int tile_mt(int rows_hint) { return rows_hint <= JG_TILE_MT8_ROWS ? 4 : 8; }
 
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                         const float* s13, const int32_t* counts, const int32_t* offsets,
                         const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                         int max_pairs, int rows_hint, hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= JG_STREAM_MAX_ROWS) {
+  if (rows_hint <= JG_STREAM_MAX_ROWS)
     return launch_gemm1_stream(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I,
                                E_l, max_pairs, stream_mt(rows_hint), stream);
-  } else {
-    constexpr int MT = 4, NW = 2;
-    const dim3 grid(m_slots(max_pairs, 16 * MT, E_l), I / (64 * NW));
-    gemm1_swiglu_kernel<MT, NW><<<grid, 256, 0, stream>>>(hs, hs_scale, w13, s13, counts,
-                                                          offsets, sorted_tok, C, T, H, I, E_l);
-  }
-  return hipGetLastError();
+  return launch_gemm1_tile(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l,
+                           max_pairs, tile_mt(rows_hint), stream);
 }
 
 hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
                         const int32_t* counts, const int32_t* offsets, const float* sorted_w,
-                        float* partial, int H, int I, int E_l, int max_pairs, int rows_hint, hipStream_t stream) {
+                        float* partial, int H, int I, int E_l, int max_pairs, int rows_hint,
+                        hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= JG_STREAM_MAX_ROWS) {
+  if (rows_hint <= JG_STREAM_MAX_ROWS)
     return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
                                max_pairs, stream_mt(rows_hint), stream);
-  } else {
-    constexpr int MT = 4, NW = 2;
-    const dim3 grid(m_slots(max_pairs, 16 * MT, E_l), H / (64 * NW));
-    gemm2_kernel<MT, NW><<<grid, 256, 0, stream>>>(C, w2, s2, counts, offsets, sorted_w, partial,
-                                                   H, I, E_l);
-  }
-  return hipGetLastError();
+  return launch_gemm2_tile(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs,
+                           tile_mt(rows_hint), stream);
 }
 
 hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
                                                     float* __restrict__ topk_w) {
   constexpr int E = VPL * kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const int t = blockIdx.x * (blockDim.x / kWave) + wave_id();
   if (t >= T) return;  // wave-uniform
 
   float x[VPL];

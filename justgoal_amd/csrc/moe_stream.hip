@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) JG_G1S_OCC void gemm1_stream_kernel(
   __shared__ float red[3][MT * 8][kWave];
   __shared__ float4 sa_lds[kMaxKB][BM / 4];  // activation scales of the tile rows, [kb][row]
   __shared__ int tok_lds[BM];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1), wave = wave_id();
   const int r16 = lane & 15, g = lane >> 4;
   const int NCT = I / 16, NKB = H / kBlock;
   const int kb0 = (NKB * wave) / 4, kb1 = (NKB * (wave + 1)) / 4;
@@ -58,7 +58,8 @@ __global__ __launch_bounds__(256) JG_G1S_OCC void gemm1_stream_kernel(
   const __amdgpu_buffer_rsrc_t ares = make_rsrc(hs, (uint32_t)T * H);
   int prev_tile = -1;
 
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+  const int stride = balanced_stride(items, gridDim.x);
+  for (int item = blockIdx.x; item < items && (int)blockIdx.x < stride; item += stride) {
     const int tile = item / NCT, ct = item % NCT;
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);
@@ -67,8 +68,9 @@ __global__ __launch_bounds__(256) JG_G1S_OCC void gemm1_stream_kernel(
     const __amdgpu_buffer_rsrc_t wres = make_rsrc(w13 + (size_t)e * 2 * I * H, 2u * I * H);
     const uint32_t woff = r16 * H + 32 * g;
     const uint32_t wsoff1 = (uint32_t)c0 * H, wsoff2 = (uint32_t)(I + c0) * H;
-    const float* sc1 = s13 + ((size_t)e * (2 * I / kBlock) + c0 / kBlock) * NKB;
-    const float* sc2 = s13 + ((size_t)e * (2 * I / kBlock) + (I + c0) / kBlock) * NKB;
+    LaneScales sc1, sc2;
+    sc1.load(s13 + ((size_t)e * (2 * I / kBlock) + c0 / kBlock) * NKB, NKB);
+    sc2.load(s13 + ((size_t)e * (2 * I / kBlock) + (I + c0) / kBlock) * NKB, NKB);
 
     // Weight loads of the first D K-blocks go out before the tile set-up below, which waits on
     // dependent global reads (token ids, then their scales).
@@ -76,8 +78,8 @@ __global__ __launch_bounds__(256) JG_G1S_OCC void gemm1_stream_kernel(
     auto load_b = [&](int kb, S1Stage<MT>& x) {
       x.b1 = buf_load32(wres, woff, wsoff1 + kb * kBlock);
       x.b2 = buf_load32(wres, woff, wsoff2 + kb * kBlock);
-      x.sw1 = sc1[kb];
-      x.sw2 = sc2[kb];
+      x.sw1 = sc1.get(kb);
+      x.sw2 = sc2.get(kb);
     };
 #pragma unroll
     for (int d = 0; d < D; ++d)
@@ -203,10 +205,10 @@ __global__ __launch_bounds__(256) JG_G2S_OCC void gemm2_stream_kernel(
   TileMap tm;
   tm.init(counts, offsets, E_l, BM);
   const int items = tm.total * NHT;
-  const int nwaves = gridDim.x * (blockDim.x / kWave);
+  const int stride = balanced_stride(items, gridDim.x * (blockDim.x / kWave));
 
-  for (int item = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; item < items;
-       item += nwaves) {
+  const int first = blockIdx.x * (blockDim.x / kWave) + wave_id();
+  for (int item = first; item < items && first < stride; item += stride) {
     const int tile = item / NHT, ht = item % NHT;
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);
@@ -220,7 +222,8 @@ __global__ __launch_bounds__(256) JG_G2S_OCC void gemm2_stream_kernel(
     }
     const __amdgpu_buffer_rsrc_t wres = make_rsrc(w2 + (size_t)e * H * I, (uint32_t)H * I);
     const uint32_t woff = r16 * I + 32 * g, wsoff = (uint32_t)h0 * I;
-    const float* sc = s2 + ((size_t)e * (H / kBlock) + h0 / kBlock) * NKB;
+    LaneScales sc;
+    sc.load(s2 + ((size_t)e * (H / kBlock) + h0 / kBlock) * NKB, NKB);
 
     v4f acc[MT];
 #pragma unroll
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(256) JG_G2S_OCC void gemm2_stream_kernel(
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int c = 0; c < 4; ++c) st.a[mt][c] = buf_load16(cres, coff[mt], 2 * (kb * kBlock + 8 * c));
-      st.sw = sc[kb];
+      st.sw = sc.get(kb);
     };
     auto compute = [&](const S2Stage<MT>& st) {
       v8bf bc[4];
