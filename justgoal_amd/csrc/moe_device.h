@@ -133,17 +133,6 @@ __device__ __forceinline__ bool find_m_tile(const int32_t* __restrict__ counts, 
   return false;
 }
 
-// Workers actually used by a persistent loop over `items` equal work items with `workers`
-// launched: the fewest workers that still need the same number of rounds, so every used worker
-// gets the same number of items and no round runs nearly empty (workers at or past the
-// returned stride do nothing). Computed on the device from the routed counts, which the host
-// never sees.
-__device__ __forceinline__ int balanced_stride(int items, int workers) {
-  if (items <= 0) return workers;
-  const int rounds = (items + workers - 1) / workers;
-  return (items + rounds - 1) / rounds;
-}
-
 // Register-resident M-tile map for persistent kernels: lane l keeps expert l + 64*j (j < 4,
 // so up to 256 local experts) with its pair count, segment offset and the inclusive prefix of
 // tile counts. Built once per wave; each lookup is a ballot plus scalar lane reads.

@@ -58,8 +58,7 @@ __global__ __launch_bounds__(256) JG_G1S_OCC void gemm1_stream_kernel(
   const __amdgpu_buffer_rsrc_t ares = make_rsrc(hs, (uint32_t)T * H);
   int prev_tile = -1;
 
-  const int stride = balanced_stride(items, gridDim.x);
-  for (int item = blockIdx.x; item < items && (int)blockIdx.x < stride; item += stride) {
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
     const int tile = item / NCT, ct = item % NCT;
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);
@@ -205,10 +204,10 @@ __global__ __launch_bounds__(256) JG_G2S_OCC void gemm2_stream_kernel(
   TileMap tm;
   tm.init(counts, offsets, E_l, BM);
   const int items = tm.total * NHT;
-  const int stride = balanced_stride(items, gridDim.x * (blockDim.x / kWave));
+  const int stride = gridDim.x * (blockDim.x / kWave);
 
   const int first = blockIdx.x * (blockDim.x / kWave) + wave_id();
-  for (int item = first; item < items && first < stride; item += stride) {
+  for (int item = first; item < items; item += stride) {
     const int tile = item / NHT, ht = item % NHT;
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);

@@ -58,8 +58,7 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
   // this thread's A staging chunks: row = (tid + 256*c) / 8, 16-byte chunk = tid % 8
   const int a_chunk = tid & 7;
 
-  const int stride = balanced_stride(items, gridDim.x);
-  for (int item = blockIdx.x; item < items && (int)blockIdx.x < stride; item += stride) {
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
     const int tile = item / NNT, nt = item % NNT;
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);
@@ -221,8 +220,7 @@ __global__ __launch_bounds__(256) void gemm2_tile_kernel(
   const __amdgpu_buffer_rsrc_t cres = make_rsrc(C, (uint32_t)max_pairs * I * 2);
   const int a_chunk = tid & 15;
 
-  const int stride = balanced_stride(items, gridDim.x);
-  for (int item = blockIdx.x; item < items && (int)blockIdx.x < stride; item += stride) {
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
     const int tile = item / NNT, nt = item % NNT;
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);
