@@ -79,23 +79,27 @@ def time_calls(call, steps, warmup, dev):
 
 def stage_times(call, reps, dev):
     """Average per-stage milliseconds from hipEvents the library records on its own stream."""
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)]
-    for e in evs:  # torch creates the underlying hipEvent on first record
-        e.record()
-    torch.cuda.synchronize(dev)
     import ctypes
-    arr = (ctypes.c_void_p * len(evs))(*[e.cuda_event for e in evs])
+    n = len(STAGES) + 1
+    sets = [[torch.cuda.Event(enable_timing=True) for _ in range(n)] for _ in range(reps)]
+    for evs in sets:  # torch creates the underlying hipEvent on first record
+        for e in evs:
+            e.record()
+    torch.cuda.synchronize(dev)
     L = _lib.lib()
     tot = [0.0] * len(STAGES)
-    _lib.check(L.moe_set_stage_events(arr, len(evs)), "moe_set_stage_events")
     try:
-        for _ in range(reps):
+        # calls go back to back (no host sync in between), as in the timed loop
+        for evs in sets:
+            arr = (ctypes.c_void_p * n)(*[e.cuda_event for e in evs])
+            _lib.check(L.moe_set_stage_events(arr, n), "moe_set_stage_events")
             call()
-            torch.cuda.synchronize(dev)
-            for i in range(len(STAGES)):
-                tot[i] += evs[i].elapsed_time(evs[i + 1])
+        torch.cuda.synchronize(dev)
     finally:
         L.moe_set_stage_events(None, 0)
+    for evs in sets:
+        for i in range(len(STAGES)):
+            tot[i] += evs[i].elapsed_time(evs[i + 1])
     return {s: tot[i] / reps for i, s in enumerate(STAGES)}
 
 
@@ -125,6 +129,14 @@ def measure(cfg, weights_dev, steps, warmup, dev, seed=0):
                           gb_s=g1_bytes / (g1_ms * 1e-3) / 1e9,
                           tflops=g1_flops / (g1_ms * 1e-3) / 1e12))
     return res, kw
+
+
+def gemm1_kernel_name(cfg):
+    """The GEMM1+SwiGLU kernel family the library picks for this shape: the shape-only rule of
+    justgoal_amd/csrc/moe_gemm.hip (expected pairs per expert T*top_k/E <= 16 -> streaming)."""
+    g = cfg.geom
+    return ("gemm1_stream_kernel" if cfg.tokens * g.top_k // g.num_experts <= 16
+            else "gemm1_tile_kernel")
 
 
 def load_traffic(name):
@@ -163,7 +175,18 @@ def main():
     ap.add_argument("--secondary", default="ds_t4096")
     ap.add_argument("--sweep", action="store_true", help="also measure ds_t16384_skew and qwen3_t1024")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 device-to-device copies of 1 GiB (reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 1 << 30, "copies": 5}))
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build runs the operator on a single MI355X "
               "(expert-parallel sharding across GPUs is a design note, not built); use --gpus 1.",
@@ -216,7 +239,7 @@ def main():
                    "hidden": cfg.geom.hidden, "intermediate": cfg.geom.intermediate,
                    "local_experts": cfg.geom.local_experts, "top_k": cfg.geom.top_k,
                    "parallelism": "single GPU (EP rank 0 of 8: local experts 0..31)"},
-        "roofline": {"bound": "hbm", "kernel": "gemm1_swiglu_kernel", "achieved": g1["gb_s"],
+        "roofline": {"bound": "hbm", "kernel": gemm1_kernel_name(cfg), "achieved": g1["gb_s"],
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": g1["gb_s"] / PEAK_HBM_GBS,
                      "traffic": load_traffic(cfg.name), "algorithmic_bytes": g1["bytes"],
                      "avg_launch_ms": g1["ms"]},
