@@ -56,8 +56,9 @@ typedef struct moe_geometry {
  *   kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t1/kernel.cu:743-790
  * and the value-returning Python entry `run(...)` it backs
  *   goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:286-288.
- * Same argument order and meaning. Difference: the workspace need not be zeroed on entry (no
- * kernel relies on its contents), and it is sized by moe_workspace_bytes(T).
+ * Same argument order and meaning. Difference: the workspace need not be zeroed on entry (the
+ * reference requires a zeroed one, t1/main.py:77-83; no kernel here keeps state in it), and it
+ * is sized by moe_workspace_bytes(T). Calls that overlap in time need distinct workspaces.
  */
 int moe_run(const void* logits, const void* bias, const void* hs, const void* hs_scale,
             const void* w13, const void* s13, const void* w2, const void* s2, int local_offset,
@@ -99,6 +100,7 @@ enum {
   MOE_WS_SORTED_W,       /* fp32  [Npmax]     routing weight of each pair */
   MOE_WS_C,              /* bf16  [Npmax, I]  SwiGLU activations */
   MOE_WS_PARTIAL,        /* fp32  [Npmax, H]  weighted GEMM2 rows */
+  MOE_WS_CHUNK_COUNTS,   /* int32 [ceil(T/16), E_l] pairs per local expert per 16-token group */
   MOE_WS_NUM_REGIONS     /* total size is written at this index */
 };
 

@@ -17,9 +17,9 @@ LIB_PATH = os.environ.get("JUSTGOAL_MOE_LIB") or os.path.join(_HERE, "libjustgoa
 EXPORTED = ("moe_run", "moe_workspace_bytes", "moe_run_ex", "moe_workspace_bytes_ex",
             "moe_route_ex", "moe_workspace_layout", "moe_set_stage_events", "moe_error_string")
 
-MOE_WS_NUM_REGIONS = 9
+MOE_WS_NUM_REGIONS = 10
 WS_REGIONS = ("topk_idx", "topk_w", "pair_of", "counts", "offsets", "sorted_tok", "sorted_w", "C",
-              "partial")
+              "partial", "chunk_counts")
 
 _LIB = None
 

@@ -61,6 +61,7 @@ void layout(const moe_geometry* g, int T, int64_t* off) {
       4 * Np,                            // sorted_w
       2 * Np * g->intermediate,          // C (bf16)
       4 * Np * g->hidden,                // partial (fp32)
+      4 * (int64_t)jgmoe::route_chunks(T) * El,  // chunk count rows
   };
   int64_t cur = 0;
   for (int i = 0; i < MOE_WS_NUM_REGIONS; ++i) {
@@ -99,6 +100,7 @@ struct Regions {
   float* sorted_w;
   uint16_t* C;
   float* partial;
+  int32_t* hist;
 };
 
 Regions carve(const moe_geometry* g, int T, void* ws) {
@@ -109,7 +111,7 @@ Regions carve(const moe_geometry* g, int T, void* ws) {
                  (int32_t*)(b + off[MOE_WS_PAIR_OF]),  (int32_t*)(b + off[MOE_WS_COUNTS]),
                  (int32_t*)(b + off[MOE_WS_OFFSETS]),  (int32_t*)(b + off[MOE_WS_SORTED_TOK]),
                  (float*)(b + off[MOE_WS_SORTED_W]),   (uint16_t*)(b + off[MOE_WS_C]),
-                 (float*)(b + off[MOE_WS_PARTIAL])};
+                 (float*)(b + off[MOE_WS_PARTIAL]), (int32_t*)(b + off[MOE_WS_CHUNK_COUNTS])};
 }
 
 #define JG_TRY(expr)                              \
@@ -126,10 +128,12 @@ int route_and_permute(const moe_geometry* g, const void* logits, const void* bia
   JG_TRY(mark_stage(0, stream));
   JG_TRY(jgmoe::launch_route((const float*)logits, (const uint16_t*)bias, T, g->num_experts,
                              g->n_group, g->topk_group, g->top_k, g->routing_method, scaling,
-                             r.topk_idx, r.topk_w, stream));
+                             local_offset, g->local_experts, r.topk_idx, r.topk_w, r.hist,
+                             stream));
   JG_TRY(mark_stage(1, stream));
-  JG_TRY(jgmoe::launch_permute(r.topk_idx, r.topk_w, T, g->top_k, local_offset, g->local_experts,
-                               r.counts, r.offsets, r.sorted_tok, r.sorted_w, r.pair_of, stream));
+  JG_TRY(jgmoe::launch_permute(r.topk_idx, r.topk_w, r.hist, T, g->top_k, local_offset,
+                               g->local_experts, r.counts, r.offsets, r.sorted_tok, r.sorted_w,
+                               r.pair_of, stream));
   JG_TRY(mark_stage(2, stream));
   return MOE_OK;
 }

@@ -9,14 +9,20 @@ namespace jgmoe {
 constexpr int ROUTING_DS = 0;
 constexpr int ROUTING_SOFTMAX = 1;
 
+// Routing. Writes topk_idx / topk_w and the count rows `hist` [route_chunks(T), E_l].
 hipError_t launch_route(const float* logits, const uint16_t* bias, int T, int E, int n_group,
-                        int topk_group, int top_k, int method, float rsf, int32_t* topk_idx,
-                        float* topk_w, hipStream_t stream);
+                        int topk_group, int top_k, int method, float rsf, int local_offset,
+                        int E_l, int32_t* topk_idx, float* topk_w, int32_t* hist,
+                        hipStream_t stream);
 
-hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, int T, int K,
-                          int local_offset, int E_l, int32_t* counts, int32_t* offsets,
-                          int32_t* sorted_tok, float* sorted_w, int32_t* pair_of,
-                          hipStream_t stream);
+// Segment layout (counts, offsets, sorted tokens/weights, pair map) from the count rows.
+hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, const int32_t* hist,
+                          int T, int K, int local_offset, int E_l, int32_t* counts,
+                          int32_t* offsets, int32_t* sorted_tok, float* sorted_w,
+                          int32_t* pair_of, hipStream_t stream);
+
+// Number of routing workgroups (16 tokens each) = rows of the chunk count table.
+int route_chunks(int T);
 
 // Grouped GEMM1 (W13) with the SwiGLU epilogue: C[p, :] = bf16(X1 * silu(X2)) for every pair p.
 // max_pairs bounds the number of pairs (sizes the grid; surplus workgroups exit at once);

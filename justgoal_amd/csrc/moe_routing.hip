@@ -1,53 +1,85 @@
 // Routing and token-permute kernels.
 //
-// route_kernel: one wave64 per token, each lane owns VPL = E/64 consecutive experts.
+// route_kernel: one wave64 per token (16 tokens per workgroup), each lane owning VPL = E/64
+//   consecutive experts.
 //   DeepSeek no-aux routing (reference semantics: goal_full_shape/fable-5.1/moe_fp8_fwd/MOEDIR/
 //   moe_common.cuh:271-365, kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t14107/
 //   moe_kernel.cu:482-600): sigmoid, + bias, group score = sum of the group's top two, keep
 //   topk_group groups (ties -> lower group), top_k experts among kept groups (ties -> lower
 //   expert), w = s / (sum s + 1e-20) * scaling. Softmax routing ranks by logit and renormalises.
-//   Everything stays in registers: group reductions are xor-shuffles inside the group's lanes and
-//   each top-k round is a 64-bit (order key, ~index) wave max.
+//   Cross-lane steps are DPP row operations plus scalar lane reads (no LDS round trips): the
+//   group top-2 merges inside the group's lanes, each top-k round is a DPP max of order keys
+//   followed by a ballot that picks the lowest lane (= lowest expert index) holding it.
+//   Each workgroup also writes its per-expert pair counts (one row of the chunk count table).
 //
-// permute_kernel: one workgroup per local expert, a deterministic stable compaction of the
-//   tokens that selected it (ascending token order = torch.nonzero order). No atomics, so the
-//   workspace needs no zeroing and the layout is identical from run to run.
+// permute_kernel: one workgroup per 64 tokens. From the count rows it derives the segment
+//   offsets and this chunk's base inside each segment, then places its pairs: a pair's rank
+//   inside its expert is a popcount over a per-expert token bitmask built with LDS atomic ORs
+//   (order-independent). Tokens end up ascending inside each expert's segment (torch.nonzero
+//   order) and the layout is identical from run to run; no global atomics, so the workspace
+//   carries no state between calls.
 #include "moe_device.h"
 #include "moe_kernels.h"
 
 namespace jgmoe {
 
-__device__ __forceinline__ unsigned long long make_key(float v, int idx) {
-  v = v + 0.0f;  // -0 -> +0 so that equal values tie on the index
-  return ((unsigned long long)float_order_key(v) << 32) | (uint32_t)(~(uint32_t)idx);
+namespace {
+
+constexpr int kRouteWaves = 16;          // tokens per routing workgroup (one wave each)
+constexpr int kPlaceTokens = 64;         // tokens per permute workgroup (one bitmask word)
+constexpr int kMaxLocal = 256;           // local experts supported by the count / scan stages
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
 }
 
+// Max over the wave: DPP reduction inside each row of 16 lanes, then four scalar lane reads.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, dpp<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = max(x, dpp<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = max(x, dpp<0x141>(x));  // row_half_mirror
+  x = max(x, dpp<0x140>(x));  // row_mirror
+  const uint32_t a = __builtin_amdgcn_readlane(x, 0), b = __builtin_amdgcn_readlane(x, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(x, 32), d = __builtin_amdgcn_readlane(x, 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Value of the partner lane for a butterfly step of width `off` inside a group of lanes whose
+// halves already hold uniform values (so a mirror pairs them as well as an xor would).
+__device__ __forceinline__ float group_partner(float v, int off) {
+  const uint32_t u = __float_as_uint(v);
+  switch (off) {
+    case 1: return __uint_as_float(dpp<0xB1>(u));
+    case 2: return __uint_as_float(dpp<0x4E>(u));
+    case 4: return __uint_as_float(dpp<0x141>(u));
+    case 8: return __uint_as_float(dpp<0x140>(u));
+    default: return __shfl_xor(v, off);
+  }
+}
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+  return float_order_key(v + 0.0f);  // -0 -> +0 so that equal values tie on the index
+}
+
+// Routes one token (all 64 lanes active). Lanes k < top_k return selection k.
 template <int VPL, int METHOD>
-__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits,
-                                                    const uint16_t* __restrict__ bias, int T,
-                                                    int n_group, int topk_group, int top_k,
-                                                    float rsf, int32_t* __restrict__ topk_idx,
-                                                    float* __restrict__ topk_w) {
+__device__ __forceinline__ void route_token(const float (&x)[VPL], const float (&bv)[VPL],
+                                            int n_group, int topk_group, int top_k, float rsf,
+                                            int& out_idx, float& out_w) {
   constexpr int E = VPL * kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * (blockDim.x / kWave) + wave_id();
-  if (t >= T) return;  // wave-uniform
-
-  float x[VPL];
-  const float* xr = logits + (size_t)t * E + lane * VPL;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) x[j] = xr[j];
-
   float s[VPL];
-  unsigned long long key[VPL];
+  uint32_t key[VPL];
+
   if (METHOD == ROUTING_DS) {
     float v[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       s[j] = (float)(1.0 / (1.0 + exp(-(double)x[j])));
-      v[j] = s[j] + (bias ? bf16_bits_to_float(bias[lane * VPL + j]) : 0.0f);
+      v[j] = s[j] + bv[j];
     }
-    // top-2 (as a multiset) of this lane's values, then of the group's lanes
+    // top-2 (as a multiset) of this lane's values, then across the group's lanes
     float m1 = -INFINITY, m2 = -INFINITY;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
@@ -58,9 +90,10 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
         m2 = v[j];
       }
     }
-    const int lpg = (E / n_group) / VPL;  // lanes per group, a power of two
+    const int gsz = E / n_group;
+    const int lpg = gsz / VPL;  // lanes per group, a power of two
     for (int off = 1; off < lpg; off <<= 1) {
-      const float o1 = __shfl_xor(m1, off), o2 = __shfl_xor(m2, off);
+      const float o1 = group_partner(m1, off), o2 = group_partner(m2, off);
       if (m1 >= o1) {
         m2 = fmaxf(m2, o1);
       } else {
@@ -68,21 +101,21 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
         m1 = o1;
       }
     }
-    const float gscore = (E / n_group > 1) ? m1 + m2 : m1;
+    const float gscore = gsz > 1 ? m1 + m2 : m1;
     const int g = lane / lpg;
     int rank = 0;
     for (int h = 0; h < n_group; ++h) {
-      const float o = __shfl(gscore, h * lpg);
+      const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), h * lpg));
       rank += (o > gscore) || (o == gscore && h < g);
     }
     const bool keep = rank < topk_group;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) key[j] = keep ? make_key(v[j], lane * VPL + j) : 0ull;
+    for (int j = 0; j < VPL; ++j) key[j] = keep ? order_key(v[j]) : 0u;
   } else {
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       s[j] = x[j];
-      key[j] = make_key(x[j], lane * VPL + j);
+      key[j] = order_key(x[j]);
     }
   }
 
@@ -93,23 +126,29 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     sel_idx[k] = 0;
     sel_val[k] = 0.f;
     if (k < top_k) {
-      unsigned long long best = key[0];
+      // this lane's best remaining candidate (larger key, then lower index)
+      uint32_t lb = key[0];
+      int lj = 0;
 #pragma unroll
-      for (int j = 1; j < VPL; ++j) best = key[j] > best ? key[j] : best;
-#pragma unroll
-      for (int off = kWave / 2; off >= 1; off >>= 1) {
-        const unsigned long long o = __shfl_xor(best, off);
-        best = o > best ? o : best;
-      }
-      const int idx = (int)(~(uint32_t)best);
+      for (int j = 1; j < VPL; ++j)
+        if (key[j] > lb) {
+          lb = key[j];
+          lj = j;
+        }
+      const uint32_t m = wave_max_u32(lb);
+      const int src = __ffsll((long long)__ballot(lb == m)) - 1;  // lowest lane = lowest index
+      const int jsel = __builtin_amdgcn_readlane(lj, src);
       float mine = s[0];
 #pragma unroll
-      for (int j = 0; j < VPL; ++j) {
-        if (lane * VPL + j == idx) key[j] = 0ull;
-        if ((idx % VPL) == j) mine = s[j];
+      for (int j = 1; j < VPL; ++j)
+        if (lj == j) mine = s[j];
+      sel_val[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), src));
+      sel_idx[k] = src * VPL + jsel;
+      if (lane == src) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+          if (j == jsel) key[j] = 0u;
       }
-      sel_idx[k] = idx;
-      sel_val[k] = __shfl(mine, idx / VPL);
     }
   }
 
@@ -133,104 +172,229 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
 #pragma unroll
     for (int k = 0; k < kMaxTopK; ++k) w[k] = ex[k] / sum;
   }
-  if (lane < top_k) {
-    int oi = sel_idx[0];
-    float ow = w[0];
+  out_idx = sel_idx[0];
+  out_w = w[0];
 #pragma unroll
-    for (int k = 1; k < kMaxTopK; ++k)
-      if (lane == k) {
-        oi = sel_idx[k];
-        ow = w[k];
-      }
-    topk_idx[(size_t)t * top_k + lane] = oi;
-    topk_w[(size_t)t * top_k + lane] = ow;
-  }
+  for (int k = 1; k < kMaxTopK; ++k)
+    if (lane == k) {
+      out_idx = sel_idx[k];
+      out_w = w[k];
+    }
 }
 
-// Block-wide sum over 256 threads (4 waves).
-__device__ __forceinline__ int block_sum_256(int v, int* red) {
-#pragma unroll
-  for (int off = kWave / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  const int wave = threadIdx.x / kWave;
-  __syncthreads();
-  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
-  __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
+
+// (token, slot) -> local expert (or -1) and routing weight, for up to kPlaceTokens tokens.
+struct TokenPairs {
+  int le[kPlaceTokens][kMaxTopK];
+  float w[kPlaceTokens][kMaxTopK];
+};
+
+__device__ __forceinline__ int local_of(int ge, int local_offset, int E_l) {
+  const int le = ge - local_offset;
+  return (le >= 0 && le < E_l) ? le : -1;
 }
 
-__global__ __launch_bounds__(256) void permute_kernel(const int32_t* __restrict__ topk_idx,
-                                                      const float* __restrict__ topk_w, int T,
-                                                      int K, int local_offset, int E_l,
-                                                      int32_t* __restrict__ counts,
-                                                      int32_t* __restrict__ offsets,
-                                                      int32_t* __restrict__ sorted_tok,
-                                                      float* __restrict__ sorted_w,
-                                                      int32_t* __restrict__ pair_of) {
-  __shared__ int red[4];
-  __shared__ int wcnt[4];
-  const int e = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1), wave = tid / kWave;
+// Token membership per local expert: bit r of bits[e] is set when token row r selected e.
+struct ExpertMasks {
+  unsigned long long bits[kMaxLocal][kPlaceTokens / 64];
+};
 
-  // pass 1: pairs of lower local experts (= this segment's offset) and of this expert
-  int lt = 0, eq = 0;
-  for (int t = tid; t < T; t += 256) {
-    for (int k = 0; k < K; ++k) {
-      const int le = topk_idx[(size_t)t * K + k] - local_offset;
-      lt += (le >= 0 && le < e);
-      eq += (le == e);
-    }
+// Builds the masks of tp rows 0..n-1 (whole workgroup; LDS atomic ORs are order-independent)
+// and cnt[e] = pairs of expert e among them. Ends with a barrier.
+__device__ __forceinline__ void build_masks(const TokenPairs& tp, int n, int top_k, int E_l,
+                                            ExpertMasks& m, int* cnt) {
+  const int words = (n + 63) / 64;
+  for (int i = threadIdx.x; i < E_l * words; i += blockDim.x) m.bits[i / words][i % words] = 0ull;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n * top_k; i += blockDim.x) {
+    const int r = i / top_k, k = i % top_k;
+    const int e = tp.le[r][k];
+    if (e >= 0) atomicOr(&m.bits[e][r >> 6], 1ull << (r & 63));
   }
-  const int base = block_sum_256(lt, red);
-  const int cnt = block_sum_256(eq, red);
-  if (tid == 0) {
-    counts[e] = cnt;
-    offsets[e] = base;
-    if (e == E_l - 1) offsets[E_l] = base + cnt;
+  __syncthreads();
+  for (int e = threadIdx.x; e < E_l; e += blockDim.x) {
+    int c = 0;
+    for (int w = 0; w < words; ++w) c += __popcll(m.bits[e][w]);
+    cnt[e] = c;
   }
+  __syncthreads();
+}
 
-  // pass 2: stable placement, 256 tokens per step
-  int running = 0;
-  for (int t0 = 0; t0 < T; t0 += 256) {
-    const int t = t0 + tid;
-    int slot = -1;
-    if (t < T) {
-      for (int k = 0; k < K; ++k) {
-        const int le = topk_idx[(size_t)t * K + k] - local_offset;
-        if (le == e) slot = k;
-        if (e == 0 && (le < 0 || le >= E_l)) pair_of[(size_t)t * K + k] = -1;
-      }
-    }
-    const unsigned long long m = __ballot(slot >= 0);
-    const int pre = __popcll(m & ((1ull << lane) - 1ull));
-    __syncthreads();
-    if (lane == 0) wcnt[wave] = __popcll(m);
-    __syncthreads();
-    int woff = 0;
-    for (int w = 0; w < wave; ++w) woff += wcnt[w];
-    const int total = wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
-    if (slot >= 0) {
-      const int p = base + running + woff + pre;
+// Places tp rows 0..n-1 (tokens t0..t0+n-1): pair (r, k) of expert e goes to base[e] plus the
+// number of earlier rows that also selected e, so each segment stays in ascending token order.
+__device__ __forceinline__ void place_from_masks(const TokenPairs& tp, const ExpertMasks& m,
+                                                 int n, int t0, int T, int top_k,
+                                                 const int* base, int32_t* __restrict__ sorted_tok,
+                                                 float* __restrict__ sorted_w,
+                                                 int32_t* __restrict__ pair_of) {
+  for (int i = threadIdx.x; i < n * top_k; i += blockDim.x) {
+    const int r = i / top_k, k = i % top_k, t = t0 + r;
+    const int e = tp.le[r][k];
+    if (e >= 0) {
+      int rank = __popcll(m.bits[e][r >> 6] & ((1ull << (r & 63)) - 1ull));
+      for (int w = 0; w < (r >> 6); ++w) rank += __popcll(m.bits[e][w]);
+      const int p = base[e] + rank;
       sorted_tok[p] = t;
-      sorted_w[p] = topk_w[(size_t)t * K + slot];
-      pair_of[(size_t)t * K + slot] = p;
+      sorted_w[p] = tp.w[r][k];
+      pair_of[(size_t)t * top_k + k] = p;
+    } else if (t < T) {
+      pair_of[(size_t)t * top_k + k] = -1;
     }
-    running += total;
   }
 }
+
+// Exclusive prefix over n <= 256 ints by one wave (4 per lane) into out[0..n].
+__device__ __forceinline__ void wave_exclusive_scan(const int* in, int* out, int n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int v[4], tot = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane * 4 + j;
+    v[j] = e < n ? in[e] : 0;
+    tot += v[j];
+  }
+  int incl = tot;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  int run = incl - tot;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane * 4 + j;
+    if (e < n) out[e] = run;
+    run += v[j];
+  }
+  if (lane == kWave - 1) out[n] = incl;
+}
+
+}  // namespace
+
+template <int VPL, int METHOD>
+__global__ __launch_bounds__(1024) void route_kernel(
+    const float* __restrict__ logits, const uint16_t* __restrict__ bias, int T, int n_group,
+    int topk_group, int top_k, float rsf, int local_offset, int E_l, int32_t* __restrict__ topk_idx,
+    float* __restrict__ topk_w, int32_t* __restrict__ hist) {
+  constexpr int E = VPL * kWave;
+  __shared__ TokenPairs tp;  // rows 0..15 used
+  __shared__ ExpertMasks masks;
+  __shared__ int cnt[kMaxLocal];
+  const int lane = threadIdx.x & (kWave - 1), wave = wave_id();
+  const int t0 = blockIdx.x * kRouteWaves;
+  const int t = t0 + wave;
+
+  int le = -1;
+  float w = 0.f;
+  if (t < T) {  // wave-uniform
+    float bv[VPL], x[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      x[j] = logits[(size_t)t * E + lane * VPL + j];
+      bv[j] = (METHOD == ROUTING_DS && bias) ? bf16_bits_to_float(bias[lane * VPL + j]) : 0.0f;
+    }
+    int idx;
+    route_token<VPL, METHOD>(x, bv, n_group, topk_group, top_k, rsf, idx, w);
+    if (lane < top_k) {
+      topk_idx[(size_t)t * top_k + lane] = idx;
+      topk_w[(size_t)t * top_k + lane] = w;
+      le = local_of(idx, local_offset, E_l);
+    }
+  }
+  if (lane < kMaxTopK) {
+    tp.le[wave][lane] = le;
+    tp.w[wave][lane] = w;
+  }
+  __syncthreads();
+  build_masks(tp, kRouteWaves, top_k, E_l, masks, cnt);
+  for (int e = threadIdx.x; e < E_l; e += blockDim.x) hist[(size_t)blockIdx.x * E_l + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(256) void permute_kernel(
+    const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w,
+    const int32_t* __restrict__ hist, int T, int K, int local_offset, int E_l, int n_rows,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_tok, float* __restrict__ sorted_w,
+    int32_t* __restrict__ pair_of) {
+  __shared__ TokenPairs tp;  // rows 0..63 used
+  __shared__ ExpertMasks masks;
+  __shared__ int chunk_cnt[kMaxLocal];
+  __shared__ int total[kMaxLocal];
+  __shared__ int before[kMaxLocal];
+  __shared__ int off[kMaxLocal + 1];
+  const int t0 = blockIdx.x * kPlaceTokens;
+  const int row0 = t0 / kRouteWaves;  // first count row of this chunk
+  // Column sums of the count table: thread (e, slice) adds every n_slices-th row of column e;
+  // loads are issued eight at a time so they overlap.
+  const int n_slices = max(1, (int)blockDim.x / E_l);
+  const int e = threadIdx.x % E_l, slice = threadIdx.x / E_l;
+  if (threadIdx.x < E_l) {
+    total[threadIdx.x] = 0;
+    before[threadIdx.x] = 0;
+  }
+  __syncthreads();
+  if (slice < n_slices) {
+    int a = 0, b = 0;
+    for (int r0 = slice; r0 < n_rows; r0 += 8 * n_slices) {
+      int h[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int r = r0 + u * n_slices;
+        h[u] = r < n_rows ? hist[(size_t)r * E_l + e] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        a += h[u];
+        b += (r0 + u * n_slices) < row0 ? h[u] : 0;
+      }
+    }
+    atomicAdd(&total[e], a);
+    atomicAdd(&before[e], b);
+  }
+  for (int i = threadIdx.x; i < kPlaceTokens * kMaxTopK; i += blockDim.x) {
+    const int r = i / kMaxTopK, k = i % kMaxTopK, t = t0 + r;
+    int l = -1;
+    float w = 0.f;
+    if (t < T && k < K) {
+      l = local_of(topk_idx[(size_t)t * K + k], local_offset, E_l);
+      w = topk_w[(size_t)t * K + k];
+    }
+    tp.le[r][k] = l;
+    tp.w[r][k] = w;
+  }
+  __syncthreads();
+  const int n = min(kPlaceTokens, T - t0);
+  build_masks(tp, n, K, E_l, masks, chunk_cnt);
+  if (wave_id() == 0) wave_exclusive_scan(total, off, E_l);
+  __syncthreads();
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= E_l; i += blockDim.x) {
+      offsets[i] = off[i];
+      if (i < E_l) counts[i] = total[i];
+    }
+  if (threadIdx.x < E_l) before[threadIdx.x] += off[threadIdx.x];
+  __syncthreads();
+  place_from_masks(tp, masks, n, t0, T, K, before, sorted_tok, sorted_w, pair_of);
+}
+
+int route_chunks(int T) { return (T + kRouteWaves - 1) / kRouteWaves; }
 
 hipError_t launch_route(const float* logits, const uint16_t* bias, int T, int E, int n_group,
-                        int topk_group, int top_k, int method, float rsf, int32_t* topk_idx,
-                        float* topk_w, hipStream_t stream) {
-  const dim3 grid((T + 3) / 4), block(256);
+                        int topk_group, int top_k, int method, float rsf, int local_offset,
+                        int E_l, int32_t* topk_idx, float* topk_w, int32_t* hist,
+                        hipStream_t stream) {
+  if (E_l > kMaxLocal || top_k > kMaxTopK) return hipErrorInvalidValue;
+  const dim3 grid(route_chunks(T)), block(kRouteWaves * kWave);
 #define JG_ROUTE(VPL)                                                                        \
   if (E == VPL * kWave) {                                                                    \
     if (method == ROUTING_DS)                                                                \
       route_kernel<VPL, ROUTING_DS><<<grid, block, 0, stream>>>(                             \
-          logits, bias, T, n_group, topk_group, top_k, rsf, topk_idx, topk_w);               \
+          logits, bias, T, n_group, topk_group, top_k, rsf, local_offset, E_l, topk_idx,     \
+          topk_w, hist);                                                                     \
     else                                                                                     \
       route_kernel<VPL, ROUTING_SOFTMAX><<<grid, block, 0, stream>>>(                        \
-          logits, bias, T, n_group, topk_group, top_k, rsf, topk_idx, topk_w);               \
+          logits, bias, T, n_group, topk_group, top_k, rsf, local_offset, E_l, topk_idx,     \
+          topk_w, hist);                                                                     \
     return hipGetLastError();                                                                \
   }
   JG_ROUTE(1)
@@ -241,13 +405,15 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, int T, int E,
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, int T, int K,
-                          int local_offset, int E_l, int32_t* counts, int32_t* offsets,
-                          int32_t* sorted_tok, float* sorted_w, int32_t* pair_of,
-                          hipStream_t stream) {
-  permute_kernel<<<dim3(E_l), dim3(256), 0, stream>>>(topk_idx, topk_w, T, K, local_offset, E_l,
-                                                      counts, offsets, sorted_tok, sorted_w,
-                                                      pair_of);
+hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, const int32_t* hist,
+                          int T, int K, int local_offset, int E_l, int32_t* counts,
+                          int32_t* offsets, int32_t* sorted_tok, float* sorted_w,
+                          int32_t* pair_of, hipStream_t stream) {
+  const int blocks = (T + kPlaceTokens - 1) / kPlaceTokens;
+  permute_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(topk_idx, topk_w, hist, T, K,
+                                                        local_offset, E_l, route_chunks(T),
+                                                        counts, offsets, sorted_tok, sorted_w,
+                                                        pair_of);
   return hipGetLastError();
 }
 

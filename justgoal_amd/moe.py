@@ -28,7 +28,7 @@ _WS: dict = {}
 
 
 def workspace(geom: Geometry, T: int, device) -> torch.Tensor:
-    """Cached uint8 workspace for (geometry, T, device); contents need no initialisation."""
+    """Cached uint8 workspace for (geometry, T, device); its contents need no initialisation."""
     dev = torch.device(device)
     key = (geom, int(T), dev)
     ws = _WS.get(key)
