@@ -22,18 +22,21 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     # packed-FP32 VALU ops are kept out of the generated code on purpose
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results straight into VGPRs: the block-scale FMAs that follow every MFMA then need
+    # no accumulator-register reads
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-result",
 ]
 
 
-def build(verbose: bool = False, out: str = LIB_PATH, defines=()) -> str:
+def build(verbose: bool = False, out: str = LIB_PATH, defines=(), extra_flags=()) -> str:
     """Compile every source into one shared library; returns its path.
 
     ``defines`` (e.g. ``["JG_G1_STREAM_D=6"]``) override the kernels' compile-time tuning knobs;
     the default build uses none."""
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
     tmp = out + f".{os.getpid()}.tmp"
-    cmd = [HIPCC, *FLAGS, *[f"-D{d}" for d in defines], "-o", tmp, *srcs]
+    cmd = [HIPCC, *FLAGS, *extra_flags, *[f"-D{d}" for d in defines], "-o", tmp, *srcs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

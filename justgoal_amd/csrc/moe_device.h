@@ -21,6 +21,19 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
 }
 
+// Marks a value the whole wave agrees on as uniform (SGPR). Needed where the compiler's
+// divergence analysis loses track, e.g. values carried across loop iterations in structs.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+template <class T>
+__device__ __forceinline__ T* uniform(T* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = uniform((uint32_t)v), hi = uniform((uint32_t)(v >> 32));
+  return (T*)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
   return __uint_as_float((uint32_t)b << 16);
 }
@@ -60,12 +73,81 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
   return uint4{(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
 }
 
+__device__ __forceinline__ uint32_t buf_load32b(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
 __device__ __forceinline__ v8i buf_load32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   typedef int v4i_ __attribute__((ext_vector_type(4)));
   const v4i_ lo = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
   const v4i_ hi = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
+
+// ---- LDS DMA (buffer_load ... lds) -------------------------------------------------------------
+// A DMA load moves 16 bytes per lane from global memory straight into LDS at
+// lds_base + 16 * lane, bypassing VGPRs; the per-lane global offsets are free, so one
+// instruction can fetch whole 128-byte lines while the LDS image gets any 16-byte permutation.
+// The compiler counts these loads in vmcnt but cannot relate them to later LDS reads, so the
+// kernels read DMA'd data with the asm reads below after an explicit vm_wait.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff,
+                                      uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_base, 16, voff, soff, 0, 0);
+}
+
+// LDS byte address of a __shared__ object, as the 32-bit value DS instructions take.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)p;
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4u ds_read16(uint32_t addr) {
+  v4u v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Completes the asm LDS reads that produced the arguments: the values flow through the wait,
+// so no use of them can be scheduled before it.
+__device__ __forceinline__ void lds_wait(v4u& x, v4u& y) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y)::"memory");
+}
+__device__ __forceinline__ void lds_wait(v4u& x, v4u& y, v4u& z, v4u& w) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x), "+v"(y), "+v"(z), "+v"(w)::"memory");
+}
+
+// Weight K-block image in LDS: 16 rows x 128 bytes, row n's 16-byte chunk c stored at position
+// c ^ ((n >> 1) & 7). A DMA instruction h (h = 0, 1) fills rows 8h..8h+7 with whole lines;
+// the MFMA operand read (lane = row n | group g, chunks 2g and 2g+1) is bank-conflict free.
+__device__ __forceinline__ int wblk_swz(int row) { return (row >> 1) & 7; }
+// Global byte offset, relative to row 0 of the block, that lane `lane` of DMA instruction h
+// fetches; `row_bytes` is the weight row pitch.
+__device__ __forceinline__ uint32_t wblk_dma_off(int lane, int h, int row_bytes) {
+  const int row = 8 * h + (lane >> 3);
+  return (uint32_t)row * row_bytes + 16 * ((lane & 7) ^ wblk_swz(row));
+}
+// LDS offsets of the two 16-byte chunks lane (n = lane & 15, g = lane >> 4) reads.
+__device__ __forceinline__ uint32_t wblk_read_off(int lane, int half) {
+  const int n = lane & 15, g = lane >> 4;
+  return n * 128 + 16 * ((2 * g + half) ^ wblk_swz(n));
+}
+
+// Marks register values as used here, so the compiler completes their loads at this point (with
+// a counted wait) instead of at a later overwrite of the same registers.
+__device__ __forceinline__ void retire(float x) { asm volatile("" ::"v"(x)); }
+__device__ __forceinline__ void retire(uint32_t x) { asm volatile("" ::"v"(x)); }
+__device__ __forceinline__ void retire(int x) { asm volatile("" ::"v"(x)); }
 
 // A row of up to 128 per-K-block scales held one per lane in two VGPRs. A K loop reads scale
 // kb with a lane read (v_readlane) instead of a scalar memory load: scalar loads complete out of

@@ -15,6 +15,18 @@
 #include "moe_device.h"
 #include "moe_kernels.h"
 
+// K-order rotation per work item (0 = off): item i walks K blocks starting at
+// (i * JG_TILE_ROT) mod (K/128), so concurrent items read different column ranges.
+#ifndef JG_TILE_ROT
+#define JG_TILE_ROT 0
+#endif
+#ifndef JG_G1T_OCC
+#define JG_G1T_OCC
+#endif
+#ifndef JG_G2T_OCC
+#define JG_G2T_OCC
+#endif
+
 namespace jgmoe {
 
 namespace {
@@ -34,7 +46,7 @@ struct BStage1 {
 }  // namespace
 
 template <int MT, int NW, int D>
-__global__ __launch_bounds__(256) void gemm1_tile_kernel(
+__global__ __launch_bounds__(256) JG_G1T_OCC void gemm1_tile_kernel(
     const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
@@ -44,7 +56,7 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
   constexpr int BM = 16 * MT;
   constexpr int ACH = MT / 2;  // 16-byte chunks per thread per K block
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * 128];
-  __shared__ __attribute__((aligned(16))) float sa_lds[2][BM];
+  __shared__ __attribute__((aligned(16))) float sa_lds[2][256];  // rows >= BM unused
   __shared__ int tok_lds[BM];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = wave_id();
@@ -54,6 +66,7 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
   tm.init(counts, offsets, E_l, BM);
   const int items = tm.total * NNT;
   const __amdgpu_buffer_rsrc_t ares = make_rsrc(hs, (uint32_t)T * H);
+  const __amdgpu_buffer_rsrc_t sres = make_rsrc(hs_scale, (uint32_t)T * (H / kBlock) * 4);
 
   // this thread's A staging chunks: row = (tid + 256*c) / 8, 16-byte chunk = tid % 8
   const int a_chunk = tid & 7;
@@ -63,6 +76,12 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);
     const int c0 = nt * 64 * NW + wave * 16 * NW;
+    const int rot = (item * JG_TILE_ROT) % NKB;
+    // K-block index of loop step kb; steps past the end map onto the last step's block.
+    auto kmap = [&](int kb) {
+      kb = min(kb, NKB - 1) + rot;
+      return kb >= NKB ? kb - NKB : kb;
+    };
 
     const __amdgpu_buffer_rsrc_t wres = make_rsrc(w13 + (size_t)e * 2 * I * H, 2u * I * H);
     const uint32_t woff = r16 * H + 32 * g;
@@ -73,6 +92,7 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
 
     BStage1<NW> bst[D];
     auto load_b = [&](int kb, BStage1<NW>& x) {
+      kb = kmap(kb);  // prefetches past the end re-read the last block, never used
 #pragma unroll
       for (int j = 0; j < NW; ++j) {
         x.b1[j] = buf_load32(wres, woff, ws1 + (uint32_t)j * 16 * H + kb * kBlock);
@@ -82,8 +102,7 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
       x.sw2 = sc2.get(kb);
     };
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d < NKB) load_b(d, bst[d]);
+    for (int d = 0; d < D; ++d) load_b(d, bst[d]);
 
     __syncthreads();  // previous item's readers of tok_lds / a_lds are done
     if (tid < BM) {
@@ -102,9 +121,11 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
     float sa_next[D];
     auto load_a = [&](int kb, int slot_unused, AStage1<MT>& x, float& sx) {
       (void)slot_unused;
+      kb = kmap(kb);
 #pragma unroll
       for (int c = 0; c < ACH; ++c) x.v[c] = buf_load16(ares, aoff[c], kb * kBlock);
-      if (tid < BM) sx = hs_scale[(size_t)kb * T + sa_tok];
+      // every thread loads (rows past BM re-read row 0) so the load count per stage is uniform
+      sx = __uint_as_float(buf_load32b(sres, (uint32_t)sa_tok * 4, (uint32_t)kb * T * 4));
     };
     auto store_a = [&](int buf, const AStage1<MT>& x, float sx) {
 #pragma unroll
@@ -112,7 +133,7 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
         const int row = (tid + 256 * c) / 8;
         *(uint4*)&a_lds[buf][row * 128 + ((a_chunk ^ (row & 7)) * 16)] = x.v[c];
       }
-      if (tid < BM) sa_lds[buf][tid] = sx;
+      sa_lds[buf][tid] = sx;  // unconditional: no divergent branch in the K loop
     };
 
     v4f acc1[MT][NW], acc2[MT][NW];
@@ -124,6 +145,8 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
         acc2[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
       }
 
+    // Weights go in as the MFMA's first operand, so lane l holds output row (l & 15) and the
+    // four columns 4*(l>>4)+i: the activation scale is then one value per lane and K block.
     auto compute = [&](int buf, const BStage1<NW>& x) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -132,58 +155,71 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
         const uint4 hi = *(const uint4*)&a_lds[buf][row * 128 + (((2 * g + 1) ^ (row & 7)) * 16)];
         const v8i a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                           (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        const float4 sa = *(const float4*)&sa_lds[buf][mt * 16 + 4 * g];
-        const float f1[4] = {sa.x * x.sw1, sa.y * x.sw1, sa.z * x.sw1, sa.w * x.sw1};
-        const float f2[4] = {sa.x * x.sw2, sa.y * x.sw2, sa.z * x.sw2, sa.w * x.sw2};
+        const float sa = sa_lds[buf][row];
+        const float f1 = sa * x.sw1, f2 = sa * x.sw2;
 #pragma unroll
         for (int j = 0; j < NW; ++j) {
-          const v4f p = mfma_f8_16x16x128(a, x.b1[j]);
-          const v4f q = mfma_f8_16x16x128(a, x.b2[j]);
+          const v4f p = mfma_f8_16x16x128(x.b1[j], a);
+          const v4f q = mfma_f8_16x16x128(x.b2[j], a);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            acc1[mt][j][i] = fmaf(p[i], f1[i], acc1[mt][j][i]);
-            acc2[mt][j][i] = fmaf(q[i], f2[i], acc2[mt][j][i]);
+            acc1[mt][j][i] = fmaf(p[i], f1, acc1[mt][j][i]);
+            acc2[mt][j][i] = fmaf(q[i], f2, acc2[mt][j][i]);
           }
         }
       }
     };
 
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d < NKB) load_a(d, d, ast[d], sa_next[d]);
+    for (int d = 0; d < D; ++d) load_a(d, d, ast[d], sa_next[d]);
     store_a(0, ast[0], sa_next[0]);
-    if (D < NKB) load_a(D, 0, ast[0], sa_next[0]);
+    load_a(D, 0, ast[0], sa_next[0]);
     __syncthreads();
-    for (int kb0 = 0; kb0 < NKB; kb0 += D) {
+    // One K block: compute from LDS buffer kb&1, prefetch block kb+D into the B ring, move
+    // block kb+1 from the A ring into the other LDS buffer and prefetch block kb+1+D into the
+    // A ring. Prefetch indices are clamped, so the step has no branches.
+    auto step = [&](int d, int kb) {
+      compute(kb & 1, bst[d]);
+      // Scheduling fences keep each prefetch where it is written: without them the scheduler
+      // sinks the loads next to their use and every K block waits on memory.
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(kb + D, bst[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      const int dn = (d + 1) % D;  // compile-time after unrolling
+      store_a((kb + 1) & 1, ast[dn], sa_next[dn]);
+      load_a(kb + 1 + D, dn, ast[dn], sa_next[dn]);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    };
+    // Whole trips of D blocks run without conditionals (a conditional load inside the loop
+    // makes the compiler wait for every outstanding load at each trip); the remainder runs
+    // after the loop.
+    const int nfull = NKB / D * D;
+    for (int kb0 = 0; kb0 < nfull; kb0 += D) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const int kb = kb0 + d;
-        if (kb < NKB) {
-          compute(kb & 1, bst[d]);
-          if (kb + D < NKB) load_b(kb + D, bst[d]);
-          if (kb + 1 < NKB) {
-            const int dn = (d + 1) % D;  // compile-time after unrolling
-            store_a((kb + 1) & 1, ast[dn], sa_next[dn]);
-            if (kb + 1 + D < NKB) load_a(kb + 1 + D, dn, ast[dn], sa_next[dn]);
+      for (int d = 0; d < D; ++d) step(d, kb0 + d);
+    }
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      if (nfull + d < NKB) step(d, nfull + d);
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = m0 + mt * 16 + r16;
+      if (r < cnt) {
+        uint16_t* crow = C + (size_t)(seg + r) * I + c0 + 4 * g;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+          uint32_t h[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float x1 = acc1[mt][j][i], x2 = acc2[mt][j][i];
+            h[i] = float_to_bf16_bits(x1 * (x2 / (1.0f + __expf(-x2))));
           }
-          __syncthreads();
+          *(uint2*)(crow + 16 * j) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
         }
       }
     }
-
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = m0 + mt * 16 + 4 * g + i;
-        if (r >= cnt) continue;
-        uint16_t* crow = C + (size_t)(seg + r) * I + c0 + r16;
-#pragma unroll
-        for (int j = 0; j < NW; ++j) {
-          const float x1 = acc1[mt][j][i], x2 = acc2[mt][j][i];
-          crow[16 * j] = float_to_bf16_bits(x1 * (x2 / (1.0f + __expf(-x2))));
-        }
-      }
   }
 }
 
@@ -203,7 +239,7 @@ struct BStage2 {
 }  // namespace
 
 template <int MT, int NW, int D>
-__global__ __launch_bounds__(256) void gemm2_tile_kernel(
+__global__ __launch_bounds__(256) JG_G2T_OCC void gemm2_tile_kernel(
     const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     const float* __restrict__ sorted_w, float* __restrict__ partial, int H, int I, int E_l,
@@ -225,6 +261,11 @@ __global__ __launch_bounds__(256) void gemm2_tile_kernel(
     int m0, cnt, seg;
     const int e = tm.find(tile, BM, m0, cnt, seg);
     const int h0 = nt * 64 * NW + wave * 16 * NW;
+    const int rot = (item * JG_TILE_ROT) % NKB;
+    auto kmap = [&](int kb) {
+      kb = min(kb, NKB - 1) + rot;
+      return kb >= NKB ? kb - NKB : kb;
+    };
 
     const __amdgpu_buffer_rsrc_t wres = make_rsrc(w2 + (size_t)e * H * I, (uint32_t)H * I);
     const uint32_t woff = r16 * I + 32 * g, wsoff = (uint32_t)h0 * I;
@@ -233,14 +274,14 @@ __global__ __launch_bounds__(256) void gemm2_tile_kernel(
 
     BStage2<NW> bst[D];
     auto load_b = [&](int kb, BStage2<NW>& x) {
+      kb = kmap(kb);  // prefetches past the end re-read the last block, never used
 #pragma unroll
       for (int j = 0; j < NW; ++j)
         x.b[j] = buf_load32(wres, woff, wsoff + (uint32_t)j * 16 * I + kb * kBlock);
       x.sw = sc.get(kb);
     };
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d < NKB) load_b(d, bst[d]);
+    for (int d = 0; d < D; ++d) load_b(d, bst[d]);
 
     uint32_t aoff[MT];
 #pragma unroll
@@ -251,6 +292,7 @@ __global__ __launch_bounds__(256) void gemm2_tile_kernel(
     }
     AStage2<MT> ast[D];
     auto load_a = [&](int kb, AStage2<MT>& x) {
+      kb = kmap(kb);
 #pragma unroll
       for (int c = 0; c < MT; ++c) x.v[c] = buf_load16(cres, aoff[c], kb * kBlock * 2);
     };
@@ -299,28 +341,31 @@ __global__ __launch_bounds__(256) void gemm2_tile_kernel(
     };
 
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d < NKB) load_a(d, ast[d]);
+    for (int d = 0; d < D; ++d) load_a(d, ast[d]);
     __syncthreads();  // previous item's LDS readers are done
     store_a(0, ast[0]);
-    if (D < NKB) load_a(D, ast[0]);
+    load_a(D, ast[0]);
     __syncthreads();
-    for (int kb0 = 0; kb0 < NKB; kb0 += D) {
+    // Same K-block step and loop split as the GEMM1 tile kernel.
+    auto step = [&](int d, int kb) {
+      compute(kb & 1, bst[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(kb + D, bst[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      const int dn = (d + 1) % D;
+      store_a((kb + 1) & 1, ast[dn]);
+      load_a(kb + 1 + D, ast[dn]);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    };
+    const int nfull = NKB / D * D;
+    for (int kb0 = 0; kb0 < nfull; kb0 += D) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
-        const int kb = kb0 + d;
-        if (kb < NKB) {
-          compute(kb & 1, bst[d]);
-          if (kb + D < NKB) load_b(kb + D, bst[d]);
-          if (kb + 1 < NKB) {
-            const int dn = (d + 1) % D;  // compile-time after unrolling
-            store_a((kb + 1) & 1, ast[dn]);
-            if (kb + 1 + D < NKB) load_a(kb + 1 + D, ast[dn]);
-          }
-          __syncthreads();
-        }
-      }
+      for (int d = 0; d < D; ++d) step(d, kb0 + d);
     }
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+      if (nfull + d < NKB) step(d, nfull + d);
 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -362,7 +407,7 @@ static int tile_grid(int per_cu, long long max_items) {
 #define JG_G2T_NW 2
 #endif
 #ifndef JG_TILE_D
-#define JG_TILE_D 3
+#define JG_TILE_D 2
 #endif
 
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
