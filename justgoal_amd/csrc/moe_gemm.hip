@@ -24,29 +24,36 @@
 
 namespace jgmoe {
 
-// One thread per (token, 8 consecutive hidden columns).
-__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
-                                                      const int32_t* __restrict__ pair_of, int T,
-                                                      int K, int H, uint16_t* __restrict__ out) {
+// Workgroup = (token, 1024 consecutive hidden columns), 8 columns per thread. Each wave reads
+// the token's K pair indices once (one lane each), orders them ascending in scalar registers
+// (pair rows ascend with the local expert, the oracle's summation order) and streams the rows.
+constexpr int kCombineThreads = 128;
+
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(
+    const float* __restrict__ partial, const int32_t* __restrict__ pair_of, int T, int K, int H,
+    uint16_t* __restrict__ out) {
   const int H8 = H / 8;
-  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (long long)T * H8) return;
-  const int t = (int)(gid / H8);
-  const int c = (int)(gid % H8) * 8;
+  const int chunks = (H8 + kCombineThreads - 1) / kCombineThreads;
+  const int t = blockIdx.x / chunks;
+  const int c8 = (blockIdx.x % chunks) * kCombineThreads + threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int q = lane < K ? pair_of[(size_t)t * K + lane] : -1;
   int p[kMaxTopK];
   int n = 0;
-  for (int k = 0; k < K; ++k) {
-    const int q = pair_of[(size_t)t * K + k];
-    if (q >= 0) {
-      // insertion into the ascending list (pair rows ascend with the local expert)
+#pragma unroll
+  for (int k = 0; k < kMaxTopK; ++k) {
+    const int v = __builtin_amdgcn_readlane(q, k);
+    if (k < K && v >= 0) {
       int j = n++;
-      while (j > 0 && p[j - 1] > q) {
+      while (j > 0 && p[j - 1] > v) {
         p[j] = p[j - 1];
         --j;
       }
-      p[j] = q;
+      p[j] = v;
     }
   }
+  if (c8 >= H8) return;
+  const int c = c8 * 8;
   float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < n; ++j) {
     const float4* src = (const float4*)(partial + (size_t)p[j] * H + c);
@@ -100,10 +107,10 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
 
 hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,
                           uint16_t* out, hipStream_t stream) {
-  const long long n = (long long)T * (H / 8);
-  if (n == 0) return hipSuccess;
-  combine_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, stream>>>(partial, pair_of, T, K, H,
-                                                                        out);
+  if (T == 0) return hipSuccess;
+  const long long chunks = (H / 8 + kCombineThreads - 1) / kCombineThreads;
+  combine_kernel<<<dim3((unsigned)(T * chunks)), kCombineThreads, 0, stream>>>(partial, pair_of, T,
+                                                                               K, H, out);
   return hipGetLastError();
 }
 
