@@ -98,6 +98,12 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds_base, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_base, 16, voff, soff, 0, 0);
 }
 
+// 4 bytes per lane (e.g. one scale per row) into LDS at lds_base + 4 * lane.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff,
+                                     uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_base, 4, voff, soff, 0, 0);
+}
+
 // LDS byte address of a __shared__ object, as the 32-bit value DS instructions take.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_ptr_t)p;
@@ -117,6 +123,19 @@ __device__ __forceinline__ v4u ds_read16(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
   return v;
 }
+
+__device__ __forceinline__ float ds_read4f(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Waits for every outstanding LDS read; follow with lds_fence on each value read by asm.
+__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Routes a value through an (ordered) asm after lds_wait_all, so no use of it can move above
+// the wait.
+__device__ __forceinline__ void lds_fence(v4u& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void lds_fence(float& x) { asm volatile("" : "+v"(x)); }
 
 // Completes the asm LDS reads that produced the arguments: the values flow through the wait,
 // so no use of them can be scheduled before it.

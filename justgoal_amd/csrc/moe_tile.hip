@@ -1,386 +1,491 @@
 // LDS-tiled grouped GEMMs for segments of tens to thousands of pairs per expert.
 //
-// A workgroup computes a BM x (64*NW) tile of one expert's output (BM = 16*MT pairs). The
-// activation rows of the tile (fp8 hidden states for GEMM1, bf16 C for GEMM2) change with K only,
-// so they are staged once per 128-wide K block in LDS (double buffered, one barrier per K block)
-// and shared by the four waves; each wave owns 16*NW output columns and streams its weight rows
-// straight from HBM into registers through a D-deep ring of buffer loads. Every weight fragment
-// feeds MT MFMAs, every LDS activation fragment feeds 2*NW (GEMM1) or NW (GEMM2) MFMAs.
+// A workgroup (4 waves) computes a BM x 64 tile of one expert's GEMM1 output (BM = 16*MT pairs;
+// for GEMM2, BM x 64*NW). Everything reaches LDS by DMA (buffer_load ... lds), so the only
+// VGPRs spent on memory are the MFMA fragments of the current K block:
 //
-// LDS rows are XOR-swizzled in 16-byte chunks (chunk ^ row) so the 16 rows an MFMA operand read
-// touches fall into distinct banks.
+// * The activation tile (BM rows x one 128-wide K block: fp8 hidden-state rows for GEMM1, bf16 C
+//   rows for GEMM2) is gathered straight from the token rows into a ring of D LDS slots shared
+//   by the four waves, each wave issuing a quarter of the DMA instructions. GEMM1 also stages the
+//   rows' activation scales (4-byte DMA).
+// * Each wave streams the weight rows of its own 16*NW output columns into a private ring.
+// * One barrier per K step: a wave waits for its own DMAs of the step's block (counted vmcnt),
+//   the barrier makes everyone's visible and frees the slot read in the previous step, which is
+//   refilled at once with the block D-1 steps ahead. The prefetch runs across item boundaries
+//   (the wave's next item is resolved one item ahead), so the stream never drains.
 //
-// Block-scale handling and the K-permutation of the bf16 MFMA are those of moe_gemm.hip.
-// Persistent grid; items are (M-tile, N-tile) with the N-tile fastest.
+// LDS images are XOR-swizzled in 16-byte chunks (the DMA lane -> global address map does the
+// permutation) so MFMA fragment reads are bank-conflict free. MFMA forms, scale handling and
+// epilogues are those of the stream kernels.
 #include "moe_device.h"
 #include "moe_kernels.h"
-
-// K-order rotation per work item (0 = off): item i walks K blocks starting at
-// (i * JG_TILE_ROT) mod (K/128), so concurrent items read different column ranges.
-#ifndef JG_TILE_ROT
-#define JG_TILE_ROT 0
-#endif
-#ifndef JG_G1T_OCC
-#define JG_G1T_OCC
-#endif
-#ifndef JG_G2T_OCC
-#define JG_G2T_OCC
-#endif
 
 namespace jgmoe {
 
 namespace {
 
-// Per-thread share of an A tile: BM rows x 128 bytes = BM*8 chunks of 16 B over 256 threads.
+constexpr int kWaves = 4;
+constexpr int kWBlk = 16 * kBlock;  // 16 weight rows x 128 bytes
+
+// vmcnt holds 6 bits; deeper counts are clamped, which only makes a wait stricter.
+constexpr int vm_depth(int n) { return n > 63 ? 63 : n < 0 ? 0 : n; }
+
+// ---- GEMM1 ------------------------------------------------------------------------------------
+
 template <int MT>
-struct AStage1 {
-  uint4 v[MT / 2 > 0 ? MT / 2 : 1];
+struct T1Item {
+  const uint8_t* wbase;   // the expert's W13
+  uint32_t wsoff;         // c0 * H (this wave's first X1 row)
+  LaneScales sc1, sc2;    // weight scales of this wave's X1 / X2 row block
+  uint32_t aoff[MT / 2];  // per lane: global offset of its A DMA chunk (token row, K 0)
+  uint32_t saoff;         // per lane: token * 4 for its activation-scale DMA
+  int m0, cnt, seg, c0;
 };
 
-template <int NW>
-struct BStage1 {
-  v8i b1[NW], b2[NW];
-  float sw1, sw2;
-};
-
-}  // namespace
-
-template <int MT, int NW, int D>
-__global__ __launch_bounds__(256) JG_G1T_OCC void gemm1_tile_kernel(
+template <int MT, int D>
+__global__ __launch_bounds__(256) void gemm1_tile_kernel(
     const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ sorted_tok, uint16_t* __restrict__ C, int T, int H, int I,
-    int E_l) {
-  static_assert(MT % 2 == 0, "A staging assumes an even number of 16-row sub-tiles");
+    int E_l, int max_pairs) {
+  static_assert(MT % 2 == 0 && MT <= 8, "A DMA splits BM rows over 4 waves, 8 rows each");
+  static_assert(D >= 3, "the prefetch lead is D-1 blocks");
   constexpr int BM = 16 * MT;
-  constexpr int ACH = MT / 2;  // 16-byte chunks per thread per K block
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * 128];
-  __shared__ __attribute__((aligned(16))) float sa_lds[2][256];  // rows >= BM unused
-  __shared__ int tok_lds[BM];
+  constexpr int AI = MT / 2;        // A DMA instructions per wave per step (8 rows x 128 B each)
+  constexpr int OPS = 4 + AI + 1;   // vector-memory operations per wave per step
+  constexpr int MW = AI + 5;        // metadata dwords per lane
+  __shared__ __attribute__((aligned(16))) uint32_t mring[kWaves][MW][kWave];
+  __shared__ __attribute__((aligned(16))) uint8_t bring[kWaves][D][2 * kWBlk];
+  __shared__ __attribute__((aligned(16))) uint8_t aring[D][BM * kBlock];
+  __shared__ __attribute__((aligned(16))) float sring[D][BM];
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = wave_id();
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int r16 = lane & 15, g = lane >> 4;
-  const int NNT = I / (64 * NW), NKB = H / kBlock;
+  const int NNT = I / 64, NKB = H / kBlock;
   TileMap tm;
   tm.init(counts, offsets, E_l, BM);
   const int items = tm.total * NNT;
+  int it = uniform((int)blockIdx.x);
+  if (it >= items) return;  // whole workgroup
+  const int stride = gridDim.x;
+
   const __amdgpu_buffer_rsrc_t ares = make_rsrc(hs, (uint32_t)T * H);
-  const __amdgpu_buffer_rsrc_t sres = make_rsrc(hs_scale, (uint32_t)T * (H / kBlock) * 4);
+  const __amdgpu_buffer_rsrc_t sares = make_rsrc(hs_scale, (uint32_t)T * NKB * 4);
+  const uint32_t dma0 = wblk_dma_off(lane, 0, H), dma1 = wblk_dma_off(lane, 1, H);
+  const uint32_t rd0 = wblk_read_off(lane, 0), rd1 = wblk_read_off(lane, 1);
+  uint8_t* my_bring = &bring[w][0][0];
 
-  // this thread's A staging chunks: row = (tid + 256*c) / 8, 16-byte chunk = tid % 8
-  const int a_chunk = tid & 7;
-
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+  // Per-lane item metadata (token ids of the rows this wave's DMAs fetch, weight-scale rows)
+  // arrives by 4-byte DMA in a small per-wave LDS area and is read back at the item switch, so
+  // the compiler tracks no loads across the K loop. A instruction i covers tile rows
+  // 8*(w*AI + i) + lane/8; the scale DMA covers row (w*64) mod BM + lane (clamped to the tile).
+  const __amdgpu_buffer_rsrc_t tokres = make_rsrc(sorted_tok, (uint32_t)max_pairs * 4);
+  const __amdgpu_buffer_rsrc_t s13res =
+      make_rsrc(s13, (uint32_t)E_l * (2 * I / kBlock) * NKB * 4);
+  uint32_t* my_meta = &mring[w][0][0];
+  auto meta = [&](int item, T1Item<MT>& x) {
+    item = uniform(item);
     const int tile = item / NNT, nt = item % NNT;
-    int m0, cnt, seg;
-    const int e = tm.find(tile, BM, m0, cnt, seg);
-    const int c0 = nt * 64 * NW + wave * 16 * NW;
-    const int rot = (item * JG_TILE_ROT) % NKB;
-    // K-block index of loop step kb; steps past the end map onto the last step's block.
-    auto kmap = [&](int kb) {
-      kb = min(kb, NKB - 1) + rot;
-      return kb >= NKB ? kb - NKB : kb;
-    };
-
-    const __amdgpu_buffer_rsrc_t wres = make_rsrc(w13 + (size_t)e * 2 * I * H, 2u * I * H);
-    const uint32_t woff = r16 * H + 32 * g;
-    const uint32_t ws1 = (uint32_t)c0 * H, ws2 = (uint32_t)(I + c0) * H;
-    LaneScales sc1, sc2;
-    sc1.load(s13 + ((size_t)e * (2 * I / kBlock) + c0 / kBlock) * NKB, NKB);
-    sc2.load(s13 + ((size_t)e * (2 * I / kBlock) + (I + c0) / kBlock) * NKB, NKB);
-
-    BStage1<NW> bst[D];
-    auto load_b = [&](int kb, BStage1<NW>& x) {
-      kb = kmap(kb);  // prefetches past the end re-read the last block, never used
+    const int e = tm.find(tile, BM, x.m0, x.cnt, x.seg);
+    x.m0 = uniform(x.m0);
+    x.cnt = uniform(x.cnt);
+    x.seg = uniform(x.seg);
+    x.c0 = uniform(nt * 64 + w * 16);
+    x.wbase = uniform(w13 + (size_t)e * 2 * I * H);
+    x.wsoff = uniform((uint32_t)x.c0 * H);
+    const int last = x.cnt - 1;
 #pragma unroll
-      for (int j = 0; j < NW; ++j) {
-        x.b1[j] = buf_load32(wres, woff, ws1 + (uint32_t)j * 16 * H + kb * kBlock);
-        x.b2[j] = buf_load32(wres, woff, ws2 + (uint32_t)j * 16 * H + kb * kBlock);
-      }
-      x.sw1 = sc1.get(kb);
-      x.sw2 = sc2.get(kb);
-    };
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_b(d, bst[d]);
-
-    __syncthreads();  // previous item's readers of tok_lds / a_lds are done
-    if (tid < BM) {
-      const int r = m0 + tid;
-      tok_lds[tid] = sorted_tok[seg + (r < cnt ? r : cnt - 1)];
+    for (int i = 0; i < AI; ++i) {
+      const int r = x.m0 + 8 * (w * AI + i) + (lane >> 3);
+      dma4(tokres, my_meta + i * kWave, 4u * (x.seg + (r < last ? r : last)), 0);
     }
-    __syncthreads();
-    uint32_t aoff[ACH];
+    // Waves whose 64 rows lie past BM repeat the rows of wave w mod (BM/64): same bytes to the
+    // same LDS words, so every wave issues the same operation count.
+    const int rs = x.m0 + (w * kWave) % BM + (lane < BM ? lane : BM - 1);
+    dma4(tokres, my_meta + AI * kWave, 4u * (x.seg + (rs < last ? rs : last)), 0);
+    const uint32_t so1 = uniform((uint32_t)((e * (2 * I / kBlock) + x.c0 / kBlock) * NKB) * 4);
+    const uint32_t so2 =
+        uniform((uint32_t)((e * (2 * I / kBlock) + (I + x.c0) / kBlock) * NKB) * 4);
+    dma4(s13res, my_meta + (AI + 1) * kWave, 4u * lane, so1);
+    dma4(s13res, my_meta + (AI + 2) * kWave, 4u * (lane + kWave), so1);
+    dma4(s13res, my_meta + (AI + 3) * kWave, 4u * lane, so2);
+    dma4(s13res, my_meta + (AI + 4) * kWave, 4u * (lane + kWave), so2);
+  };
+  // Reads back the per-lane metadata of the last meta() (its DMAs must have completed).
+  auto finish = [&](T1Item<MT>& x) {
+    const uint32_t mb = lds_addr(my_meta) + 4 * lane;
+    float v[MW];
 #pragma unroll
-    for (int c = 0; c < ACH; ++c) aoff[c] = (uint32_t)tok_lds[(tid + 256 * c) / 8] * H + 16 * a_chunk;
-    const int sa_tok = tid < BM ? tok_lds[tid] : 0;
+    for (int j = 0; j < MW; ++j) v[j] = ds_read4f(mb + j * 4 * kWave);
+    lds_wait_all();
+#pragma unroll
+    for (int j = 0; j < MW; ++j) lds_fence(v[j]);
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+      const int row = 8 * (w * AI + i) + (lane >> 3);
+      x.aoff[i] = __float_as_uint(v[i]) * H + 16 * ((lane & 7) ^ wblk_swz(row));
+    }
+    x.saoff = __float_as_uint(v[AI]) * 4;
+    x.sc1.v0 = v[AI + 1];
+    x.sc1.v1 = v[AI + 2];
+    x.sc2.v0 = v[AI + 3];
+    x.sc2.v1 = v[AI + 4];
+  };
 
-    // A ring: slot d holds the activation chunks (and this row's scale) of a K block kb with
-    // kb % D == d, loaded D blocks ahead of its compute.
-    AStage1<MT> ast[D];
-    float sa_next[D];
-    auto load_a = [&](int kb, int slot_unused, AStage1<MT>& x, float& sx) {
-      (void)slot_unused;
-      kb = kmap(kb);
-#pragma unroll
-      for (int c = 0; c < ACH; ++c) x.v[c] = buf_load16(ares, aoff[c], kb * kBlock);
-      // every thread loads (rows past BM re-read row 0) so the load count per stage is uniform
-      sx = __uint_as_float(buf_load32b(sres, (uint32_t)sa_tok * 4, (uint32_t)kb * T * 4));
-    };
-    auto store_a = [&](int buf, const AStage1<MT>& x, float sx) {
-#pragma unroll
-      for (int c = 0; c < ACH; ++c) {
-        const int row = (tid + 256 * c) / 8;
-        *(uint4*)&a_lds[buf][row * 128 + ((a_chunk ^ (row & 7)) * 16)] = x.v[c];
-      }
-      sa_lds[buf][tid] = sx;  // unconditional: no divergent branch in the K loop
-    };
+  T1Item<MT> cur, nxt, nn;
+  meta(it, cur);
+  vm_wait<0>();
+  finish(cur);
+  int it_n = it + stride;
+  meta(it_n < items ? it_n : it, nxt);
+  vm_wait<0>();
+  finish(nxt);
 
-    v4f acc1[MT][NW], acc2[MT][NW];
+  auto issue = [&](bool second, int kbi, int slot) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int j = 0; j < NW; ++j) {
-        acc1[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        acc2[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
-      }
+    for (int i = 0; i < AI; ++i)
+      dma16(ares, &aring[slot][(w * AI + i) * 1024], second ? nxt.aoff[i] : cur.aoff[i],
+            (uint32_t)kbi * kBlock);
+    dma4(sares, &sring[slot][(w * kWave) % BM], second ? nxt.saoff : cur.saoff,
+         (uint32_t)kbi * T * 4);
+    const __amdgpu_buffer_rsrc_t wres =
+        make_rsrc(uniform(second ? nxt.wbase : cur.wbase), 2u * I * H);
+    const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
+    uint8_t* b = my_bring + slot * 2 * kWBlk;
+    dma16(wres, b, dma0, ws);
+    dma16(wres, b + 1024, dma1, ws);
+    dma16(wres, b + kWBlk, dma0, ws + (uint32_t)I * H);
+    dma16(wres, b + kWBlk + 1024, dma1, ws + (uint32_t)I * H);
+  };
 
-    // Weights go in as the MFMA's first operand, so lane l holds output row (l & 15) and the
-    // four columns 4*(l>>4)+i: the activation scale is then one value per lane and K block.
-    auto compute = [&](int buf, const BStage1<NW>& x) {
+  // Blocks 0..D-2 of the first item; block s+D-1 is issued at step s.
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int row = mt * 16 + r16;
-        const uint4 lo = *(const uint4*)&a_lds[buf][row * 128 + (((2 * g) ^ (row & 7)) * 16)];
-        const uint4 hi = *(const uint4*)&a_lds[buf][row * 128 + (((2 * g + 1) ^ (row & 7)) * 16)];
-        const v8i a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                          (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        const float sa = sa_lds[buf][row];
-        const float f1 = sa * x.sw1, f2 = sa * x.sw2;
+  for (int d = 0; d < D - 1; ++d) {
+    issue(false, d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  int slot = 0;  // ring slot of the next block to compute (a running step count mod D)
+  for (;;) {
+    const int it_nn = it_n + stride;
+    meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
+
+    v4f acc1[MT], acc2[MT];
 #pragma unroll
-        for (int j = 0; j < NW; ++j) {
-          const v4f p = mfma_f8_16x16x128(x.b1[j], a);
-          const v4f q = mfma_f8_16x16x128(x.b2[j], a);
+    for (int mt = 0; mt < MT; ++mt) {
+      acc1[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+      acc2[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    }
+    int kb = 0;
+    do {
+      {
+        const int d = slot;
+        vm_wait<vm_depth((D - 2) * OPS)>();  // this wave's DMAs of block kb are done
+        // Everyone's are, and everyone has finished reading slot d-1. A bare s_barrier: the
+        // fence of __syncthreads would wait for every DMA in flight.
+        __builtin_amdgcn_s_barrier();
+        const int kn = kb + D - 1;
+        const bool second = kn >= NKB;
+        issue(second, second ? kn - NKB : kn, d == 0 ? D - 1 : d - 1);
+        __builtin_amdgcn_sched_barrier(0);
+
+        const uint32_t bb = lds_addr(my_bring + d * 2 * kWBlk);
+        const uint32_t ab = lds_addr(&aring[d][0]);
+        const uint32_t sb = lds_addr(&sring[d][0]);
+        v4u x1l = ds_read16(bb + rd0), x1h = ds_read16(bb + rd1);
+        v4u x2l = ds_read16(bb + kWBlk + rd0), x2h = ds_read16(bb + kWBlk + rd1);
+        v4u al[MT], ah[MT];
+        float sa[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          al[mt] = ds_read16(ab + mt * kWBlk + rd0);
+          ah[mt] = ds_read16(ab + mt * kWBlk + rd1);
+          sa[mt] = ds_read4f(sb + 4 * (mt * 16 + r16));
+        }
+        lds_wait_all();
+        lds_fence(x1l);
+        lds_fence(x1h);
+        lds_fence(x2l);
+        lds_fence(x2h);
+        const v8i b1 = v8i{(int)x1l[0], (int)x1l[1], (int)x1l[2], (int)x1l[3],
+                           (int)x1h[0], (int)x1h[1], (int)x1h[2], (int)x1h[3]};
+        const v8i b2 = v8i{(int)x2l[0], (int)x2l[1], (int)x2l[2], (int)x2l[3],
+                           (int)x2h[0], (int)x2h[1], (int)x2h[2], (int)x2h[3]};
+        const float sw1 = cur.sc1.get(kb), sw2 = cur.sc2.get(kb);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          lds_fence(al[mt]);
+          lds_fence(ah[mt]);
+          lds_fence(sa[mt]);
+          const v8i a = v8i{(int)al[mt][0], (int)al[mt][1], (int)al[mt][2], (int)al[mt][3],
+                            (int)ah[mt][0], (int)ah[mt][1], (int)ah[mt][2], (int)ah[mt][3]};
+          const float f1 = sa[mt] * sw1, f2 = sa[mt] * sw2;
+          const v4f p = mfma_f8_16x16x128(b1, a);
+          const v4f q = mfma_f8_16x16x128(b2, a);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            acc1[mt][j][i] = fmaf(p[i], f1, acc1[mt][j][i]);
-            acc2[mt][j][i] = fmaf(q[i], f2, acc2[mt][j][i]);
+            acc1[mt][i] = fmaf(p[i], f1, acc1[mt][i]);
+            acc2[mt][i] = fmaf(q[i], f2, acc2[mt][i]);
           }
         }
       }
-    };
-
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_a(d, d, ast[d], sa_next[d]);
-    store_a(0, ast[0], sa_next[0]);
-    load_a(D, 0, ast[0], sa_next[0]);
-    __syncthreads();
-    // One K block: compute from LDS buffer kb&1, prefetch block kb+D into the B ring, move
-    // block kb+1 from the A ring into the other LDS buffer and prefetch block kb+1+D into the
-    // A ring. Prefetch indices are clamped, so the step has no branches.
-    auto step = [&](int d, int kb) {
-      compute(kb & 1, bst[d]);
-      // Scheduling fences keep each prefetch where it is written: without them the scheduler
-      // sinks the loads next to their use and every K block waits on memory.
-      __builtin_amdgcn_sched_barrier(0);
-      load_b(kb + D, bst[d]);
-      __builtin_amdgcn_sched_barrier(0);
-      const int dn = (d + 1) % D;  // compile-time after unrolling
-      store_a((kb + 1) & 1, ast[dn], sa_next[dn]);
-      load_a(kb + 1 + D, dn, ast[dn], sa_next[dn]);
-      __builtin_amdgcn_sched_barrier(0);
-      __syncthreads();
-    };
-    // Whole trips of D blocks run without conditionals (a conditional load inside the loop
-    // makes the compiler wait for every outstanding load at each trip); the remainder runs
-    // after the loop.
-    const int nfull = NKB / D * D;
-    for (int kb0 = 0; kb0 < nfull; kb0 += D) {
-#pragma unroll
-      for (int d = 0; d < D; ++d) step(d, kb0 + d);
-    }
-#pragma unroll
-    for (int d = 0; d < D - 1; ++d)
-      if (nfull + d < NKB) step(d, nfull + d);
+      slot = slot + 1 == D ? 0 : slot + 1;
+      ++kb;
+    } while (kb < NKB);
+    // Everything but the next item's prefetched blocks is complete, the metadata DMAs included.
+    vm_wait<vm_depth((D - 1) * OPS)>();
+    finish(nn);
 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int r = m0 + mt * 16 + r16;
-      if (r < cnt) {
-        uint16_t* crow = C + (size_t)(seg + r) * I + c0 + 4 * g;
+      const int r = cur.m0 + mt * 16 + r16;
+      if (r < cur.cnt) {
+        uint32_t h[4];
 #pragma unroll
-        for (int j = 0; j < NW; ++j) {
-          uint32_t h[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float x1 = acc1[mt][j][i], x2 = acc2[mt][j][i];
-            h[i] = float_to_bf16_bits(x1 * (x2 / (1.0f + __expf(-x2))));
-          }
-          *(uint2*)(crow + 16 * j) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        for (int i = 0; i < 4; ++i) {
+          const float x1 = acc1[mt][i], x2 = acc2[mt][i];
+          h[i] = float_to_bf16_bits(x1 * (x2 / (1.0f + __expf(-x2))));
         }
+        *(uint2*)(C + (size_t)(cur.seg + r) * I + cur.c0 + 4 * g) =
+            uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
       }
     }
+    if (it_n >= items) break;
+    it = it_n;
+    it_n = it_nn;
+    cur = nxt;
+    nxt = nn;
   }
+  vm_wait<0>();  // no DMA may still target this workgroup's LDS when it retires
 }
 
-namespace {
+// ---- GEMM2 ------------------------------------------------------------------------------------
 
-template <int MT>
-struct AStage2 {
-  uint4 v[MT];  // BM rows x 256 bytes = BM*16 chunks over 256 threads
+template <int MT, int NW>
+struct T2Item {
+  const uint8_t* wbase;  // the expert's W2
+  uint32_t wsoff;        // h0 * I (this wave's first W2 row)
+  LaneScales sc[NW];     // weight scales of this wave's row blocks
+  uint32_t aoff[MT];     // per lane: byte offset of its C DMA chunk (pair row, K 0)
+  float wgt[MT];         // routing weight of the lane's output row in each sub-tile
+  int m0, cnt, seg, h0;
 };
-
-template <int NW>
-struct BStage2 {
-  v8i b[NW];
-  float sw;
-};
-
-}  // namespace
 
 template <int MT, int NW, int D>
-__global__ __launch_bounds__(256) JG_G2T_OCC void gemm2_tile_kernel(
+__global__ __launch_bounds__(256) void gemm2_tile_kernel(
     const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     const float* __restrict__ sorted_w, float* __restrict__ partial, int H, int I, int E_l,
     int max_pairs) {
+  static_assert(D >= 3, "the prefetch lead is D-1 blocks");
   constexpr int BM = 16 * MT;
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * 256];
+  constexpr int ARow = 2 * kBlock;   // bf16 C bytes per row per K block
+  constexpr int OPS = 2 * NW + MT;   // per wave per step: W2 DMAs + C DMAs (4 rows x 256 B each)
+  constexpr int MW = MT + 2 * NW;    // metadata dwords per lane
+  __shared__ __attribute__((aligned(16))) uint32_t mring[kWaves][MW][kWave];
+  __shared__ __attribute__((aligned(16))) uint8_t bring[kWaves][D][NW * kWBlk];
+  __shared__ __attribute__((aligned(16))) uint8_t aring[D][BM * ARow];
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = wave_id();
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int r16 = lane & 15, g = lane >> 4;
   const int NNT = H / (64 * NW), NKB = I / kBlock;
   TileMap tm;
   tm.init(counts, offsets, E_l, BM);
   const int items = tm.total * NNT;
+  int it = uniform((int)blockIdx.x);
+  if (it >= items) return;
+  const int stride = gridDim.x;
+
   const __amdgpu_buffer_rsrc_t cres = make_rsrc(C, (uint32_t)max_pairs * I * 2);
-  const int a_chunk = tid & 15;
+  const uint32_t dma0 = wblk_dma_off(lane, 0, I), dma1 = wblk_dma_off(lane, 1, I);
+  const uint32_t rd0 = wblk_read_off(lane, 0), rd1 = wblk_read_off(lane, 1);
+  uint8_t* my_bring = &bring[w][0][0];
 
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+  // C DMA instruction i of wave w covers tile rows 4*(w*MT + i) + lane/16, 16-byte chunk
+  // position lane & 15 holding chunk (lane & 15) ^ (row & 15). Per-lane metadata (routing
+  // weights of the lane's output rows, weight-scale rows) comes by 4-byte DMA into a per-wave
+  // LDS area and is read back at the item switch.
+  const __amdgpu_buffer_rsrc_t wgtres = make_rsrc(sorted_w, (uint32_t)max_pairs * 4);
+  const __amdgpu_buffer_rsrc_t s2res = make_rsrc(s2, (uint32_t)E_l * (H / kBlock) * NKB * 4);
+  uint32_t* my_meta = &mring[w][0][0];
+  auto meta = [&](int item, T2Item<MT, NW>& x) {
+    item = uniform(item);
     const int tile = item / NNT, nt = item % NNT;
-    int m0, cnt, seg;
-    const int e = tm.find(tile, BM, m0, cnt, seg);
-    const int h0 = nt * 64 * NW + wave * 16 * NW;
-    const int rot = (item * JG_TILE_ROT) % NKB;
-    auto kmap = [&](int kb) {
-      kb = min(kb, NKB - 1) + rot;
-      return kb >= NKB ? kb - NKB : kb;
-    };
-
-    const __amdgpu_buffer_rsrc_t wres = make_rsrc(w2 + (size_t)e * H * I, (uint32_t)H * I);
-    const uint32_t woff = r16 * I + 32 * g, wsoff = (uint32_t)h0 * I;
-    LaneScales sc;
-    sc.load(s2 + ((size_t)e * (H / kBlock) + h0 / kBlock) * NKB, NKB);
-
-    BStage2<NW> bst[D];
-    auto load_b = [&](int kb, BStage2<NW>& x) {
-      kb = kmap(kb);  // prefetches past the end re-read the last block, never used
+    const int e = tm.find(tile, BM, x.m0, x.cnt, x.seg);
+    x.m0 = uniform(x.m0);
+    x.cnt = uniform(x.cnt);
+    x.seg = uniform(x.seg);
+    x.h0 = uniform(nt * 64 * NW + w * 16 * NW);
+    x.wbase = uniform(w2 + (size_t)e * H * I);
+    x.wsoff = uniform((uint32_t)x.h0 * I);
+    const int last = x.cnt - 1;
 #pragma unroll
-      for (int j = 0; j < NW; ++j)
-        x.b[j] = buf_load32(wres, woff, wsoff + (uint32_t)j * 16 * I + kb * kBlock);
-      x.sw = sc.get(kb);
-    };
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_b(d, bst[d]);
-
-    uint32_t aoff[MT];
-#pragma unroll
-    for (int c = 0; c < MT; ++c) {
-      const int row = (tid + 256 * c) / 16;
-      const int r = m0 + row;
-      aoff[c] = ((uint32_t)(seg + (r < cnt ? r : cnt - 1)) * I) * 2 + 16 * a_chunk;
+    for (int i = 0; i < MT; ++i) {
+      const int row = 4 * (w * MT + i) + (lane >> 4);
+      const int r = x.m0 + row;
+      x.aoff[i] = ((uint32_t)(x.seg + (r < last ? r : last)) * I) * 2 +
+                  16 * ((lane & 15) ^ (row & 15));
     }
-    AStage2<MT> ast[D];
-    auto load_a = [&](int kb, AStage2<MT>& x) {
-      kb = kmap(kb);
 #pragma unroll
-      for (int c = 0; c < MT; ++c) x.v[c] = buf_load16(cres, aoff[c], kb * kBlock * 2);
-    };
-    auto store_a = [&](int buf, const AStage2<MT>& x) {
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = x.m0 + mt * 16 + r16;
+      dma4(wgtres, my_meta + mt * kWave, 4u * (x.seg + (r < last ? r : last)), 0);
+    }
 #pragma unroll
-      for (int c = 0; c < MT; ++c) {
-        const int row = (tid + 256 * c) / 16;
-        *(uint4*)&a_lds[buf][row * 256 + ((a_chunk ^ (row & 15)) * 16)] = x.v[c];
-      }
-    };
+    for (int j = 0; j < NW; ++j) {
+      const uint32_t so = uniform(
+          (uint32_t)(((size_t)e * (H / kBlock) + (x.h0 + 16 * j) / kBlock) * NKB) * 4);
+      dma4(s2res, my_meta + (MT + 2 * j) * kWave, 4u * lane, so);
+      dma4(s2res, my_meta + (MT + 2 * j + 1) * kWave, 4u * (lane + kWave), so);
+    }
+  };
+  auto finish = [&](T2Item<MT, NW>& x) {
+    const uint32_t mb = lds_addr(my_meta) + 4 * lane;
+    float v[MW];
+#pragma unroll
+    for (int j = 0; j < MW; ++j) v[j] = ds_read4f(mb + j * 4 * kWave);
+    lds_wait_all();
+#pragma unroll
+    for (int j = 0; j < MW; ++j) lds_fence(v[j]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) x.wgt[mt] = v[mt];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      x.sc[j].v0 = v[MT + 2 * j];
+      x.sc[j].v1 = v[MT + 2 * j + 1];
+    }
+  };
+
+  T2Item<MT, NW> cur, nxt, nn;
+  meta(it, cur);
+  vm_wait<0>();
+  finish(cur);
+  int it_n = it + stride;
+  meta(it_n < items ? it_n : it, nxt);
+  vm_wait<0>();
+  finish(nxt);
+
+  auto issue = [&](bool second, int kbi, int slot) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      dma16(cres, &aring[slot][(w * MT + i) * 1024], second ? nxt.aoff[i] : cur.aoff[i],
+            (uint32_t)kbi * ARow);
+    const __amdgpu_buffer_rsrc_t wres =
+        make_rsrc(uniform(second ? nxt.wbase : cur.wbase), (uint32_t)H * I);
+    const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
+    uint8_t* b = my_bring + slot * NW * kWBlk;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      dma16(wres, b + j * kWBlk, dma0, ws + (uint32_t)j * 16 * I);
+      dma16(wres, b + j * kWBlk + 1024, dma1, ws + (uint32_t)j * 16 * I);
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    issue(false, d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int slot = 0;  // ring slot of the next block to compute (a running step count mod D)
+  for (;;) {
+    const int it_nn = it_n + stride;
+    meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
 
     v4f acc[MT][NW];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int j = 0; j < NW; ++j) acc[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    int kb = 0;
+    do {
+      {
+        const int d = slot;
+        vm_wait<vm_depth((D - 2) * OPS)>();
+        __builtin_amdgcn_s_barrier();
+        const int kn = kb + D - 1;
+        const bool second = kn >= NKB;
+        issue(second, second ? kn - NKB : kn, d == 0 ? D - 1 : d - 1);
+        __builtin_amdgcn_sched_barrier(0);
 
-    auto compute = [&](int buf, const BStage2<NW>& x) {
-      v8bf bc[NW][4];
-#pragma unroll
-      for (int j = 0; j < NW; ++j)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          v2bf p0, p1, p2, p3;
-          fp8x4_to_bf16x4(x.b[j][2 * c], p0, p1);
-          fp8x4_to_bf16x4(x.b[j][2 * c + 1], p2, p3);
-          bc[j][c] = v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-        }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int row = mt * 16 + r16;
-        v8bf a[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          a[c] = __builtin_bit_cast(
-              v8bf, *(const uint4*)&a_lds[buf][row * 256 + (((4 * g + c) ^ (row & 15)) * 16)]);
+        const uint32_t bb = lds_addr(my_bring + d * NW * kWBlk);
+        const uint32_t ab = lds_addr(&aring[d][0]);
+        v4u wl[NW], wh[NW];
 #pragma unroll
         for (int j = 0; j < NW; ++j) {
-          v4f t = {0.f, 0.f, 0.f, 0.f};
+          wl[j] = ds_read16(bb + j * kWBlk + rd0);
+          wh[j] = ds_read16(bb + j * kWBlk + rd1);
+        }
+        v4u a[MT][4];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) t = mfma_bf16_16x16x32(a[c], bc[j][c], t);
+        for (int mt = 0; mt < MT; ++mt) {
+          const int row = mt * 16 + r16;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(t[i], x.sw, acc[mt][j][i]);
+          for (int c = 0; c < 4; ++c)
+            a[mt][c] = ds_read16(ab + row * ARow + 16 * ((4 * g + c) ^ (row & 15)));
+        }
+        lds_wait_all();
+        v8bf bw[NW][4];
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+          lds_fence(wl[j]);
+          lds_fence(wh[j]);
+          const uint32_t wv[8] = {wl[j][0], wl[j][1], wl[j][2], wl[j][3],
+                                  wh[j][0], wh[j][1], wh[j][2], wh[j][3]};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v2bf p0, p1, p2, p3;
+            fp8x4_to_bf16x4((int)wv[2 * c], p0, p1);
+            fp8x4_to_bf16x4((int)wv[2 * c + 1], p2, p3);
+            bw[j][c] = v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+          }
+        }
+        float sw[NW];
+#pragma unroll
+        for (int j = 0; j < NW; ++j) sw[j] = cur.sc[j].get(kb);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) lds_fence(a[mt][c]);
+#pragma unroll
+          for (int j = 0; j < NW; ++j) {
+            v4f t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              t = mfma_bf16_16x16x32(bw[j][c], __builtin_bit_cast(v8bf, a[mt][c]), t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(t[i], sw[j], acc[mt][j][i]);
+          }
         }
       }
-    };
+      slot = slot + 1 == D ? 0 : slot + 1;
+      ++kb;
+    } while (kb < NKB);
+    vm_wait<vm_depth((D - 1) * OPS)>();
+    finish(nn);
 
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_a(d, ast[d]);
-    __syncthreads();  // previous item's LDS readers are done
-    store_a(0, ast[0]);
-    load_a(D, ast[0]);
-    __syncthreads();
-    // Same K-block step and loop split as the GEMM1 tile kernel.
-    auto step = [&](int d, int kb) {
-      compute(kb & 1, bst[d]);
-      __builtin_amdgcn_sched_barrier(0);
-      load_b(kb + D, bst[d]);
-      __builtin_amdgcn_sched_barrier(0);
-      const int dn = (d + 1) % D;
-      store_a((kb + 1) & 1, ast[dn]);
-      load_a(kb + 1 + D, ast[dn]);
-      __builtin_amdgcn_sched_barrier(0);
-      __syncthreads();
-    };
-    const int nfull = NKB / D * D;
-    for (int kb0 = 0; kb0 < nfull; kb0 += D) {
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = cur.m0 + mt * 16 + r16;
+      if (r < cur.cnt) {
+        const float wp = cur.wgt[mt];
+        float* orow = partial + (size_t)(cur.seg + r) * H + cur.h0 + 4 * g;
 #pragma unroll
-      for (int d = 0; d < D; ++d) step(d, kb0 + d);
-    }
-#pragma unroll
-    for (int d = 0; d < D - 1; ++d)
-      if (nfull + d < NKB) step(d, nfull + d);
-
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = m0 + mt * 16 + 4 * g + i;
-        if (r >= cnt) continue;
-        const int p = seg + r;
-        const float wp = sorted_w[p];
-        float* orow = partial + (size_t)p * H + h0 + r16;
-#pragma unroll
-        for (int j = 0; j < NW; ++j) orow[16 * j] = acc[mt][j][i] * wp;
+        for (int j = 0; j < NW; ++j)
+          *(float4*)(orow + 16 * j) = float4{acc[mt][j][0] * wp, acc[mt][j][1] * wp,
+                                             acc[mt][j][2] * wp, acc[mt][j][3] * wp};
       }
+    }
+    if (it_n >= items) break;
+    it = it_n;
+    it_n = it_nn;
+    cur = nxt;
+    nxt = nn;
   }
+  vm_wait<0>();
 }
+
+}  // namespace
 
 static int tile_grid(int per_cu, long long max_items) {
   static int cus = 0;
@@ -397,53 +502,67 @@ static int tile_grid(int per_cu, long long max_items) {
   return g < 1 ? 1 : (int)g;
 }
 
-#ifndef JG_TILE_PER_CU
-#define JG_TILE_PER_CU 2
-#endif
-#ifndef JG_G1T_NW
-#define JG_G1T_NW 1
-#endif
+// Workgroups per CU that fit the LDS rings (160 KiB per CU).
+static inline int tile_groups_per_cu(int lds_bytes) {
+  const int n = (160 * 1024) / lds_bytes;
+  return n < 1 ? 1 : n > 4 ? 4 : n;
+}
+
+static inline long long tile_count(int max_pairs, int bm, int E_l) {
+  return (max_pairs + bm - 1) / bm + (E_l < max_pairs ? E_l : max_pairs);
+}
+
 #ifndef JG_G2T_NW
-#define JG_G2T_NW 2
+#define JG_G2T_NW 1
 #endif
-#ifndef JG_TILE_D
-#define JG_TILE_D 2
+
+// Ring depths (lead D-1 blocks). D = 3 keeps two workgroups per CU within the 160 KiB of LDS,
+// which measured faster than deeper rings at one workgroup per CU.
+#ifndef JG_G1T_D
+#define JG_G1T_D 3
+#endif
+#ifndef JG_G2T_D
+#define JG_G2T_D 3
 #endif
 
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                              const float* s13, const int32_t* counts, const int32_t* offsets,
                              const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                              int max_pairs, int mt, hipStream_t stream) {
-#define JG_G1T(MT, NW)                                                                        \
-  {                                                                                           \
-    const long long tiles = (max_pairs + 16 * MT - 1) / (16 * MT) + (E_l < max_pairs ? E_l : max_pairs); \
-    const int grid = tile_grid(JG_TILE_PER_CU, tiles * (I / (64 * NW)));                      \
-    gemm1_tile_kernel<MT, NW, JG_TILE_D><<<grid, 256, 0, stream>>>(                           \
-        hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l);                \
+#define JG_G1T(MT, D)                                                                           \
+  {                                                                                             \
+    constexpr int lds = kWaves * D * 2 * kWBlk + D * 16 * MT * kBlock + D * 16 * MT * 4 +      \
+                        kWaves * (MT / 2 + 5) * kWave * 4;                                       \
+    const int grid =                                                                            \
+        tile_grid(tile_groups_per_cu(lds), tile_count(max_pairs, 16 * MT, E_l) * (I / 64));     \
+    gemm1_tile_kernel<MT, D><<<grid, kWaves * kWave, 0, stream>>>(                              \
+        hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs);       \
+    return hipGetLastError();                                                                   \
   }
-  if (mt <= 2) JG_G1T(2, JG_G1T_NW)
-  else if (mt <= 4) JG_G1T(4, JG_G1T_NW)
-  else JG_G1T(8, JG_G1T_NW)
+  if (mt <= 2) JG_G1T(2, JG_G1T_D)
+  if (mt <= 4) JG_G1T(4, JG_G1T_D)
+  JG_G1T(8, (JG_G1T_D > 4 ? 4 : JG_G1T_D))  // a 128-row tile leaves room for 4 slots
 #undef JG_G1T
-  return hipGetLastError();
 }
 
 hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* s2,
                              const int32_t* counts, const int32_t* offsets,
                              const float* sorted_w, float* partial, int H, int I, int E_l,
                              int max_pairs, int mt, hipStream_t stream) {
-#define JG_G2T(MT, NW)                                                                        \
-  {                                                                                           \
-    const long long tiles = (max_pairs + 16 * MT - 1) / (16 * MT) + (E_l < max_pairs ? E_l : max_pairs); \
-    const int grid = tile_grid(JG_TILE_PER_CU, tiles * (H / (64 * NW)));                      \
-    gemm2_tile_kernel<MT, NW, JG_TILE_D><<<grid, 256, 0, stream>>>(                           \
-        C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs);                 \
+#define JG_G2T(MT, NW, D)                                                                        \
+  {                                                                                              \
+    constexpr int lds = kWaves * D * NW * kWBlk + D * 16 * MT * 2 * kBlock +                     \
+                        kWaves * (MT + 2 * NW) * kWave * 4;                                      \
+    const int grid = tile_grid(tile_groups_per_cu(lds),                                          \
+                               tile_count(max_pairs, 16 * MT, E_l) * (H / (64 * NW)));           \
+    gemm2_tile_kernel<MT, NW, D><<<grid, kWaves * kWave, 0, stream>>>(                           \
+        C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs);                    \
+    return hipGetLastError();                                                                    \
   }
-  if (mt <= 2) JG_G2T(2, JG_G2T_NW)
-  else if (mt <= 4) JG_G2T(4, JG_G2T_NW)
-  else JG_G2T(8, JG_G2T_NW)
+  // BM is capped at 64 here: a 128-row bf16 ring would not fit next to the weight rings.
+  if (mt <= 2) JG_G2T(2, JG_G2T_NW, JG_G2T_D)
+  JG_G2T(4, JG_G2T_NW, JG_G2T_D)
 #undef JG_G2T
-  return hipGetLastError();
 }
 
 }  // namespace jgmoe
