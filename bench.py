@@ -103,8 +103,9 @@ def stage_times(call, reps, dev):
     return {s: tot[i] / reps for i, s in enumerate(STAGES)}
 
 
-def measure(cfg, weights_dev, steps, warmup, dev, seed=0):
+def measure(cfg, weights_dev, steps, warmup, dev, seed=None):
     geom = cfg.geom
+    seed = cfg.seed if seed is None else seed
     act = jin.make_activations(geom, cfg.tokens, seed=seed, device=dev,
                                skew_experts=cfg.skew_experts, skew_offset=cfg.skew_offset)
     w13, s13, w2, s2 = weights_dev

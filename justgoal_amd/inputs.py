@@ -30,14 +30,23 @@ class Config:
     tokens: int
     skew_experts: int = 0      # number of local experts whose logits get +skew_offset
     skew_offset: float = 0.0
+    seed: int = 0              # activation seed of the measured workload
 
+
+# The measured workloads use seed 2. The routing bias is one draw per seed, and it sets how many
+# of a token's picks land in the local group (experts 0..31): over seeds 0..31 the T=64 batch
+# gets a median of 55 local pairs on 16 experts and the T=4096 batch 3537 pairs on 27 experts.
+# Seed 2 sits at that median (55 / 16 and 4066 / 26); seed 0 is the lightest draw of the 32
+# (18 / 8 and 1299 / 21) and stays the seed of the T=16 plumbing case and its fixtures.
+BENCH_SEED = 2
 
 CONFIGS = {
     "ds_t16": Config("ds_t16", DS_V3, 16),
-    "ds_t64": Config("ds_t64", DS_V3, 64),
-    "ds_t4096": Config("ds_t4096", DS_V3, 4096),
-    "ds_t16384_skew": Config("ds_t16384_skew", DS_V3, 16384, skew_experts=8, skew_offset=3.0),
-    "qwen3_t1024": Config("qwen3_t1024", QWEN3, 1024),
+    "ds_t64": Config("ds_t64", DS_V3, 64, seed=BENCH_SEED),
+    "ds_t4096": Config("ds_t4096", DS_V3, 4096, seed=BENCH_SEED),
+    "ds_t16384_skew": Config("ds_t16384_skew", DS_V3, 16384, skew_experts=8, skew_offset=3.0,
+                             seed=BENCH_SEED),
+    "qwen3_t1024": Config("qwen3_t1024", QWEN3, 1024, seed=BENCH_SEED),
 }
 
 
@@ -96,11 +105,13 @@ def make_activations(geom: Geometry, T: int, seed: int = 0, device="cpu", skew_e
                 hidden_states=hs.to(device), hidden_states_scale=hs_scale.to(device))
 
 
-def make_inputs(cfg: Config | str, seed: int = 0, device="cpu", tokens: int | None = None,
-                weights=None):
-    """All ten operator arguments (reference names) for a configuration."""
+def make_inputs(cfg: Config | str, seed: int | None = None, device="cpu",
+                tokens: int | None = None, weights=None):
+    """All ten operator arguments (reference names) for a configuration (seed: the config's)."""
     if isinstance(cfg, str):
         cfg = CONFIGS[cfg]
+    if seed is None:
+        seed = cfg.seed
     geom = cfg.geom
     T = cfg.tokens if tokens is None else tokens
     d = make_activations(geom, T, seed, device, cfg.skew_experts, cfg.skew_offset)

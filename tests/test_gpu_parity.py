@@ -168,6 +168,14 @@ def test_qwen3_config4_t1024(gpu):
     check_case(QWEN3, 1024, gpu, seed=0, tokens_checked=256)
 
 
+@pytest.mark.parametrize("name", ["ds_t64", "ds_t4096", "ds_t16384_skew", "qwen3_t1024"])
+def test_measured_workloads(name, gpu):
+    """The exact batches bench.py times (the configs' own seed)."""
+    cfg = jin.CONFIGS[name]
+    skew = (cfg.skew_experts, cfg.skew_offset) if cfg.skew_experts else (0, 0.0)
+    check_case(cfg.geom, cfg.tokens, gpu, seed=cfg.seed, tokens_checked=128, skew=skew)
+
+
 def test_deterministic(gpu):
     """Two calls on the same inputs give bit-identical outputs (no atomics anywhere)."""
     w = weights_for(MINI_DS, gpu)[1]
