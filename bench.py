@@ -235,8 +235,11 @@ def main():
         "metric": METRIC, "value": head["tflops"], "unit": "TFLOPS", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms_per_call"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8-e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
-        "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights, 128x128 block scales)",
+        "data": f"synthetic (seed {cfg.seed}: N(0,1) activations/logits, N(0,0.1) bias, "
+                "N(0,0.02) weights, 128x128 block scales)",
         "config": {"workload": cfg.name, "geometry": cfg.geom.name, "tokens": cfg.tokens,
+                   "seed": cfg.seed, "local_pairs": head["pairs"],
+                   "active_local_experts": head["active_experts"],
                    "hidden": cfg.geom.hidden, "intermediate": cfg.geom.intermediate,
                    "local_experts": cfg.geom.local_experts, "top_k": cfg.geom.top_k,
                    "parallelism": "single GPU (EP rank 0 of 8: local experts 0..31)"},
