@@ -73,6 +73,11 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 #define JG_STREAM_MAX_ROWS 16
 #endif
 
+// Expected pairs per expert from which the large-tile kernels take over.
+#ifndef JG_BIG_ROWS
+#define JG_BIG_ROWS 64
+#endif
+
 #ifndef JG_G2T_MT
 #define JG_G2T_MT 0
 #endif
@@ -93,6 +98,11 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t*
   if (rows_hint <= JG_STREAM_MAX_ROWS)
     return launch_gemm1_stream(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I,
                                E_l, max_pairs, stream_mt(rows_hint), stream);
+  if (rows_hint >= JG_BIG_ROWS) {
+    const hipError_t b = launch_gemm1_big(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C,
+                                          T, H, I, E_l, max_pairs, stream);
+    if (b != hipErrorNotSupported) return b;
+  }
   const hipError_t e = launch_gemm1_tile(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C,
                                          T, H, I, E_l, max_pairs, tile_mt(rows_hint), stream);
   if (e != hipErrorNotSupported) return e;
@@ -108,6 +118,11 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
   if (rows_hint <= JG_STREAM_MAX_ROWS)
     return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
                                max_pairs, stream_mt(rows_hint), stream);
+  if (rows_hint >= JG_BIG_ROWS) {
+    const hipError_t b = launch_gemm2_big(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
+                                          max_pairs, stream);
+    if (b != hipErrorNotSupported) return b;
+  }
   const hipError_t e = launch_gemm2_tile(C, w2, s2, counts, offsets, sorted_w, partial, H, I,
                                          E_l, max_pairs, JG_G2T_MT ? JG_G2T_MT : tile_mt(rows_hint),
                                          stream);
