@@ -20,6 +20,13 @@
 #include "moe_device.h"
 #include "moe_kernels.h"
 
+#ifndef JG_ABL_NODMA
+#define JG_ABL_NODMA 0
+#endif
+#ifndef JG_ABL_NOMMA
+#define JG_ABL_NOMMA 0
+#endif
+
 namespace jgmoe {
 
 namespace {
@@ -39,8 +46,6 @@ constexpr int vm_depth(int n) { return n > 63 ? 63 : n < 0 ? 0 : n; }
 // block have landed (then it refills the slot freed by the previous step), the compute waves
 // before reading the block.
 
-constexpr int kComputeWaves = 4;
-constexpr int kProducer = 4;  // wave index of the producer
 
 struct B1Scalars {
   const uint8_t* wbase;  // the expert's W13
@@ -49,8 +54,10 @@ struct B1Scalars {
 };
 
 // MS: 16-row sub-tiles per compute wave (BM = 32*MS); NS: 16-column sub-tiles (BN = 32*NS).
-template <int MS, int NS, int D>
-__global__ __launch_bounds__(320) void gemm1_big_kernel(
+// MS/NS: 16-row/16-column sub-tiles per compute wave; WM x WN compute waves (wave index w:
+// wm = w % WM, wn = w / WM), so BM = 16*MS*WM and BN = 16*NS*WN; wave WM*WN is the producer.
+template <int MS, int NS, int D, int WM, int WN>
+__global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
     const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale,
     const uint8_t* __restrict__ w13, const float* __restrict__ s13,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
@@ -58,7 +65,8 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
     int E_l, int max_pairs) {
   static_assert(D >= 3, "the prefetch lead is D-1 blocks");
   static_assert(16 * NS <= kBlock && kBlock % (16 * NS) == 0, "a wave's columns share one scale block");
-  constexpr int BM = 32 * MS, BN = 32 * NS;
+  constexpr int BM = 16 * MS * WM, BN = 16 * NS * WN;
+  constexpr int kComputeWaves = WM * WN, kProducer = WM * WN;
   constexpr int AI = BM / 8;        // A DMA instructions per step (8 rows x 128 B each)
   constexpr int SI = BM / 64;       // activation-scale DMA instructions per step
   constexpr int BI = 2 * BN / 8;    // B DMA instructions per step
@@ -72,17 +80,17 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
 
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int NNT = I / BN, NKB = H / kBlock;
-  TileMap tm;
-  tm.init(counts, offsets, E_l, BM);
-  const int items = tm.total * NNT;
+  __shared__ TileMapLds tml;
+  const int items = uniform(tml.build(counts, offsets, E_l, BM, w == 0)) * NNT;
   int it = uniform((int)blockIdx.x);
   if (it >= items) return;  // whole workgroup
+  __syncthreads();  // whole workgroup
   const int stride = gridDim.x;
 
   auto scalars = [&](int item, B1Scalars& x) {
     item = uniform(item);
     const int tile = item / NNT, nt = item % NNT;
-    x.e = uniform(tm.find(tile, BM, x.m0, x.cnt, x.seg));
+    x.e = uniform(tml.template find<BM>(tile, E_l, x.m0, x.cnt, x.seg));
     x.m0 = uniform(x.m0);
     x.cnt = uniform(x.cnt);
     x.seg = uniform(x.seg);
@@ -136,15 +144,14 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
     vm_wait<0>();
     finish(nxt);
 
-    auto issue = [&](bool second, int kbi, int slot) {
-      const P& x = second ? nxt : cur;
+    auto issue = [&](const P& x, int kbi, int slot) {
 #pragma unroll
       for (int j = 0; j < AI; ++j)
-        dma16(ares, &aring[slot][j * 1024], second ? nxt.aoff[j] : cur.aoff[j],
+        dma16(ares, &aring[slot][j * 1024], x.aoff[j],
               (uint32_t)kbi * kBlock);
 #pragma unroll
       for (int k = 0; k < SI; ++k)
-        dma4(sares, &sring[slot][k * kWave], second ? nxt.saoff[k] : cur.saoff[k],
+        dma4(sares, &sring[slot][k * kWave], x.saoff[k],
              (uint32_t)kbi * T * 4);
       const __amdgpu_buffer_rsrc_t wres = make_rsrc(uniform(x.s.wbase), 2u * I * H);
       const uint32_t c0 = uniform(x.s.c0);
@@ -158,7 +165,7 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
     };
 #pragma unroll
     for (int d = 0; d < D - 1; ++d) {
-      issue(false, d, d);
+      if (!JG_ABL_NODMA) issue(cur, d, d);
       __builtin_amdgcn_sched_barrier(0);
     }
     int slot = 0;
@@ -171,7 +178,13 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
         __builtin_amdgcn_s_barrier();
         const int kn = kb + D - 1;
         const bool second = kn >= NKB;
-        issue(second, second ? kn - NKB : kn, slot == 0 ? D - 1 : slot - 1);
+        // a uniform branch, so the per-lane offsets are not selected op by op
+        if (!JG_ABL_NODMA) {
+          if (second)
+            issue(nxt, kn - NKB, slot == 0 ? D - 1 : slot - 1);
+          else
+            issue(cur, kn, slot == 0 ? D - 1 : slot - 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
         slot = slot + 1 == D ? 0 : slot + 1;
         ++kb;
@@ -184,12 +197,13 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
       cur = nxt;
       nxt = nn;
     }
+    __builtin_amdgcn_s_barrier();  // pairs with the compute waves' barrier after their last block
     vm_wait<0>();  // no DMA may still target this workgroup's LDS when it retires
     return;
   }
 
   // ---------------- compute waves ----------------
-  const int wm = w & 1, wn = w >> 1;
+  const int wm = w % WM, wn = w / WM;
   const int r16 = lane & 15, g = lane >> 4;
   const __amdgpu_buffer_rsrc_t s13res = make_rsrc(s13, (uint32_t)E_l * (2 * I / kBlock) * NKB * 4);
   const uint32_t rd0 = wblk_read_off(lane, 0), rd1 = wblk_read_off(lane, 1);
@@ -230,7 +244,48 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
   vm_wait<0>();
   finish(nxt);
 
+  // Software pipeline. The fragments a step needs first (A sub-tiles 0 and 1, the first column
+  // sub-tile of B, the activation scales) are read during the previous step; the remaining A
+  // sub-tiles are read under the first column sub-tile's MFMAs and each further B column
+  // sub-tile under the previous one's. The step's barrier for the next block sits between the
+  // two MFMA halves of the last column sub-tile, when every read of the current slot is done.
+  static_assert(MS >= 2 && NS % 2 == 0, "pipeline shape");
+  v4u al[MS], ah[MS];  // A fragments of the step, per 16-row sub-tile
+  v4u bq[2][4];        // B fragments (X1 lo/hi, X2 lo/hi) of two column sub-tiles
+  float sa[MS];        // activation scales of the lane's rows
+  auto a_base = [&](int d) { return lds_addr(&aring[d][0]) + wm * MS * kWBlk; };
+  auto b_base = [&](int d) { return lds_addr(&bring[d][0]) + wn * NS * kWBlk; };
+  auto read_a = [&](uint32_t ab, int ms) {
+    al[ms] = ds_read16(ab + ms * kWBlk + rd0);
+    ah[ms] = ds_read16(ab + ms * kWBlk + rd1);
+  };
+  auto read_b = [&](uint32_t bb, int ns, v4u(&b)[4]) {
+    b[0] = ds_read16(bb + ns * kWBlk + rd0);
+    b[1] = ds_read16(bb + ns * kWBlk + rd1);
+    b[2] = ds_read16(bb + (BN / 16 + ns) * kWBlk + rd0);
+    b[3] = ds_read16(bb + (BN / 16 + ns) * kWBlk + rd1);
+  };
+  auto read_head = [&](int d) {  // what the first MFMAs of a step need
+    const uint32_t ab = a_base(d);
+    read_a(ab, 0);
+    read_a(ab, 1);
+    read_b(b_base(d), 0, bq[0]);
+    const uint32_t sb = lds_addr(&sring[d][0]) + 4 * (wm * MS * 16 + r16);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) sa[ms] = ds_read4f(sb + 4 * 16 * ms);
+  };
+  auto fence_a = [&](int ms) {
+    lds_fence(al[ms]);
+    lds_fence(ah[ms]);
+  };
+  auto fence_b = [&](v4u(&b)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lds_fence(b[i]);
+  };
+
   int slot = 0;
+  __builtin_amdgcn_s_barrier();  // block 0 has landed
+  read_head(0);
   for (;;) {
     const int it_nn = it_n + stride;
     meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
@@ -244,68 +299,69 @@ __global__ __launch_bounds__(320) void gemm1_big_kernel(
       }
     int kb = 0;
     do {
-      const int d = slot;
-      __builtin_amdgcn_s_barrier();  // block kb is in slot d; everyone is done with slot d-1
-      const uint32_t ab = lds_addr(&aring[d][0]) + wm * MS * kWBlk;
-      const uint32_t bb = lds_addr(&bring[d][0]) + wn * NS * kWBlk;
-      const uint32_t sb = lds_addr(&sring[d][0]) + 4 * (wm * MS * 16 + r16);
-      v4u b1l[NS], b1h[NS], b2l[NS], b2h[NS];
-#pragma unroll
-      for (int ns = 0; ns < NS; ++ns) {
-        b1l[ns] = ds_read16(bb + ns * kWBlk + rd0);
-        b1h[ns] = ds_read16(bb + ns * kWBlk + rd1);
-        b2l[ns] = ds_read16(bb + (BN / 16 + ns) * kWBlk + rd0);
-        b2h[ns] = ds_read16(bb + (BN / 16 + ns) * kWBlk + rd1);
-      }
-      v4u al = ds_read16(ab + rd0), ah = ds_read16(ab + rd1);
-      float sa = ds_read4f(sb);
+      const int d = slot, dn = slot + 1 == D ? 0 : slot + 1;
+      const uint32_t ab = a_base(d), bb = b_base(d);
       const float sw1 = cur.sc1.get(kb), sw2 = cur.sc2.get(kb);
-      lds_wait_all();
-      v8i b1[NS], b2[NS];
-#pragma unroll
-      for (int ns = 0; ns < NS; ++ns) {
-        lds_fence(b1l[ns]);
-        lds_fence(b1h[ns]);
-        lds_fence(b2l[ns]);
-        lds_fence(b2h[ns]);
-        b1[ns] = v8i{(int)b1l[ns][0], (int)b1l[ns][1], (int)b1l[ns][2], (int)b1l[ns][3],
-                     (int)b1h[ns][0], (int)b1h[ns][1], (int)b1h[ns][2], (int)b1h[ns][3]};
-        b2[ns] = v8i{(int)b2l[ns][0], (int)b2l[ns][1], (int)b2l[ns][2], (int)b2l[ns][3],
-                     (int)b2h[ns][0], (int)b2h[ns][1], (int)b2h[ns][2], (int)b2h[ns][3]};
-      }
-      lds_fence(al);
-      lds_fence(ah);
-      lds_fence(sa);
-      // Software pipeline over the MS sub-tiles: sub-tile ms+1's fragments are read while
-      // sub-tile ms runs its MFMAs.
+      lds_wait_all();  // the head fragments (read during the previous step) have landed
+      fence_a(0);
+      fence_a(1);
+      fence_b(bq[0]);
+      float f1[MS], f2[MS];
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) {
-        const v8i a = v8i{(int)al[0], (int)al[1], (int)al[2], (int)al[3],
-                          (int)ah[0], (int)ah[1], (int)ah[2], (int)ah[3]};
-        const float f1 = sa * sw1, f2 = sa * sw2;
-        if (ms + 1 < MS) {
-          al = ds_read16(ab + (ms + 1) * kWBlk + rd0);
-          ah = ds_read16(ab + (ms + 1) * kWBlk + rd1);
-          sa = ds_read4f(sb + 4 * 16 * (ms + 1));
-        }
+        lds_fence(sa[ms]);
+        f1[ms] = sa[ms] * sw1;
+        f2[ms] = sa[ms] * sw2;
+      }
+      auto mma = [&](int ms, int ns, const v4u(&b)[4]) {
+        const v8i a = v8i{(int)al[ms][0], (int)al[ms][1], (int)al[ms][2], (int)al[ms][3],
+                          (int)ah[ms][0], (int)ah[ms][1], (int)ah[ms][2], (int)ah[ms][3]};
+        const v8i b1 = v8i{(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3],
+                           (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]};
+        const v8i b2 = v8i{(int)b[2][0], (int)b[2][1], (int)b[2][2], (int)b[2][3],
+                           (int)b[3][0], (int)b[3][1], (int)b[3][2], (int)b[3][3]};
+        const v4f p = mfma_f8_16x16x128(b1, a);
+        const v4f q = mfma_f8_16x16x128(b2, a);
 #pragma unroll
-        for (int ns = 0; ns < NS; ++ns) {
-          const v4f p = mfma_f8_16x16x128(b1[ns], a);
-          const v4f q = mfma_f8_16x16x128(b2[ns], a);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc1[ms][ns][i] = fmaf(p[i], f1, acc1[ms][ns][i]);
-            acc2[ms][ns][i] = fmaf(q[i], f2, acc2[ms][ns][i]);
-          }
+        for (int i = 0; i < 4; ++i) {
+          acc1[ms][ns][i] = fmaf(p[i], f1[ms], acc1[ms][ns][i]);
+          acc2[ms][ns][i] = fmaf(q[i], f2[ms], acc2[ms][ns][i]);
         }
-        if (ms + 1 < MS) {
+      };
+      // column sub-tile 0: the other A sub-tiles and B column sub-tile 1 arrive meanwhile
+#pragma unroll
+      for (int ms = 2; ms < MS; ++ms) read_a(ab, ms);
+      read_b(bb, 1, bq[1]);
+      mma(0, 0, bq[0]);
+      mma(1, 0, bq[0]);
+      lds_wait_all();
+#pragma unroll
+      for (int ms = 2; ms < MS; ++ms) fence_a(ms);
+      fence_b(bq[1]);
+#pragma unroll
+      for (int ms = 2; ms < MS; ++ms) mma(ms, 0, bq[0]);
+#pragma unroll
+      for (int ns = 1; ns < NS; ++ns) {
+        v4u(&b)[4] = bq[ns & 1];
+        if (ns + 1 < NS) {
+          read_b(bb, ns + 1, bq[(ns + 1) & 1]);
+#pragma unroll
+          for (int ms = 0; ms < MS; ++ms) mma(ms, ns, b);
           lds_wait_all();
-          lds_fence(al);
-          lds_fence(ah);
-          lds_fence(sa);
+          fence_b(bq[(ns + 1) & 1]);
+        } else {
+          // last column sub-tile (bq[1]; bq[0] is free for the next block's head)
+          mma(0, ns, b);
+          mma(1, ns, b);
+          // Block kb+1 has landed and slot d is no longer read. After the last block this
+          // barrier pairs with the producer's final one and the head read is unused.
+          __builtin_amdgcn_s_barrier();
+          read_head(dn);
+#pragma unroll
+          for (int ms = 2; ms < MS; ++ms) mma(ms, ns, b);
         }
       }
-      slot = slot + 1 == D ? 0 : slot + 1;
+      slot = dn;
       ++kb;
     } while (kb < NKB);
     vm_wait<0>();  // only this item's scale-row DMAs (and older stores) are outstanding
@@ -346,15 +402,18 @@ struct B2Scalars {
   int e, m0, cnt, seg;
 };
 
-template <int MS, int NS, int D>
-__global__ __launch_bounds__(320) void gemm2_big_kernel(
+// MS/NS: 16-row/16-column sub-tiles per compute wave; WM x WN compute waves (wave index w:
+// wm = w % WM, wn = w / WM), so BM = 16*MS*WM and BN = 16*NS*WN; wave WM*WN is the producer.
+template <int MS, int NS, int D, int WM, int WN>
+__global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     const float* __restrict__ sorted_w, float* __restrict__ partial, int H, int I, int E_l,
     int max_pairs) {
   static_assert(D >= 3, "the prefetch lead is D-1 blocks");
   static_assert(16 * NS <= kBlock && kBlock % (16 * NS) == 0, "a wave's columns share one scale block");
-  constexpr int BM = 32 * MS, BN = 32 * NS;
+  constexpr int BM = 16 * MS * WM, BN = 16 * NS * WN;
+  constexpr int kComputeWaves = WM * WN, kProducer = WM * WN;
   constexpr int ARow = 2 * kBlock;    // bf16 C bytes per row per K block
   constexpr int AI = BM / 4;          // C DMA instructions per step (4 rows x 256 B each)
   constexpr int BI = BN / 8;          // W2 DMA instructions per step (8 rows x 128 B each)
@@ -367,17 +426,17 @@ __global__ __launch_bounds__(320) void gemm2_big_kernel(
 
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int NNT = H / BN, NKB = I / kBlock;
-  TileMap tm;
-  tm.init(counts, offsets, E_l, BM);
-  const int items = tm.total * NNT;
+  __shared__ TileMapLds tml;
+  const int items = uniform(tml.build(counts, offsets, E_l, BM, w == 0)) * NNT;
   int it = uniform((int)blockIdx.x);
-  if (it >= items) return;
+  if (it >= items) return;  // whole workgroup
+  __syncthreads();
   const int stride = gridDim.x;
 
   auto scalars = [&](int item, B2Scalars& x) {
     item = uniform(item);
     const int tile = item / NNT, nt = item % NNT;
-    x.e = uniform(tm.find(tile, BM, x.m0, x.cnt, x.seg));
+    x.e = uniform(tml.template find<BM>(tile, E_l, x.m0, x.cnt, x.seg));
     x.m0 = uniform(x.m0);
     x.cnt = uniform(x.cnt);
     x.seg = uniform(x.seg);
@@ -387,36 +446,31 @@ __global__ __launch_bounds__(320) void gemm2_big_kernel(
   int it_n = it + stride;
 
   if (w == kProducer) {
-    const __amdgpu_buffer_rsrc_t cres = make_rsrc(C, (uint32_t)max_pairs * I * 2);
     const uint32_t dma0 = wblk_dma_off(lane, 0, I), dma1 = wblk_dma_off(lane, 1, I);
-    struct P {
-      B2Scalars s;
-      uint32_t aoff[AI];
-    };
     // C DMA instruction j covers tile rows 4j + lane/16, chunk position lane & 15 holding
-    // chunk (lane & 15) ^ (row & 15).
-    auto meta = [&](int item, P& x) {
-      scalars(item, x.s);
-      const int last = x.s.cnt - 1;
+    // chunk (lane & 15) ^ (row & 15). The offsets are relative to the tile's first row and the
+    // same for every item: each item's buffer resource starts at that row and ends at the
+    // segment's last row, so rows past the segment are out of range (never fetched).
+    uint32_t aoff[AI];
 #pragma unroll
-      for (int j = 0; j < AI; ++j) {
-        const int row = 4 * j + (lane >> 4);
-        const int r = x.s.m0 + row;
-        x.aoff[j] = ((uint32_t)(x.s.seg + (r < last ? r : last)) * I) * 2 +
-                    16 * ((lane & 15) ^ (row & 15));
-      }
-    };
-    P cur, nxt, nn;
-    meta(it, cur);
-    meta(it_n < items ? it_n : it, nxt);
+    for (int j = 0; j < AI; ++j) {
+      const int row = 4 * j + (lane >> 4);
+      aoff[j] = (uint32_t)row * I * 2 + 16 * ((lane & 15) ^ (row & 15));
+    }
+    B2Scalars cur, nxt, nn;
+    scalars(it, cur);
+    scalars(it_n < items ? it_n : it, nxt);
     auto issue = [&](bool second, int kbi, int slot) {
-      const P& x = second ? nxt : cur;
+      const B2Scalars& x = second ? nxt : cur;
+      const int m0 = uniform(x.m0);
+      const __amdgpu_buffer_rsrc_t cres =
+          make_rsrc(uniform(C + (size_t)(uniform(x.seg) + m0) * I),
+                    uniform((uint32_t)(uniform(x.cnt) - m0) * I * 2));
 #pragma unroll
       for (int j = 0; j < AI; ++j)
-        dma16(cres, &aring[slot][j * 1024], second ? nxt.aoff[j] : cur.aoff[j],
-              (uint32_t)kbi * ARow);
-      const __amdgpu_buffer_rsrc_t wres = make_rsrc(uniform(x.s.wbase), (uint32_t)H * I);
-      const uint32_t h0 = uniform(x.s.h0);
+        dma16(cres, &aring[slot][j * 1024], aoff[j], (uint32_t)kbi * ARow);
+      const __amdgpu_buffer_rsrc_t wres = make_rsrc(uniform(x.wbase), (uint32_t)H * I);
+      const uint32_t h0 = uniform(x.h0);
 #pragma unroll
       for (int j = 0; j < BI; ++j)
         dma16(wres, &bring[slot][j * 1024], (j & 1) ? dma1 : dma0,
@@ -424,20 +478,20 @@ __global__ __launch_bounds__(320) void gemm2_big_kernel(
     };
 #pragma unroll
     for (int d = 0; d < D - 1; ++d) {
-      issue(false, d, d);
+      if (!JG_ABL_NODMA) issue(false, d, d);
       __builtin_amdgcn_sched_barrier(0);
     }
     int slot = 0;
     for (;;) {
       const int it_nn = it_n + stride;
-      meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
+      scalars(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
       int kb = 0;
       do {
         vm_wait<vm_depth((D - 2) * OPS)>();
         __builtin_amdgcn_s_barrier();
         const int kn = kb + D - 1;
         const bool second = kn >= NKB;
-        issue(second, second ? kn - NKB : kn, slot == 0 ? D - 1 : slot - 1);
+        if (!JG_ABL_NODMA) issue(second, second ? kn - NKB : kn, slot == 0 ? D - 1 : slot - 1);
         __builtin_amdgcn_sched_barrier(0);
         slot = slot + 1 == D ? 0 : slot + 1;
         ++kb;
@@ -448,11 +502,12 @@ __global__ __launch_bounds__(320) void gemm2_big_kernel(
       cur = nxt;
       nxt = nn;
     }
+    __builtin_amdgcn_s_barrier();  // pairs with the compute waves' barrier after their last block
     vm_wait<0>();
     return;
   }
 
-  const int wm = w & 1, wn = w >> 1;
+  const int wm = w % WM, wn = w / WM;
   const int r16 = lane & 15, g = lane >> 4;
   const __amdgpu_buffer_rsrc_t wgtres = make_rsrc(sorted_w, (uint32_t)max_pairs * 4);
   const __amdgpu_buffer_rsrc_t s2res = make_rsrc(s2, (uint32_t)E_l * (H / kBlock) * NKB * 4);
@@ -498,7 +553,30 @@ __global__ __launch_bounds__(320) void gemm2_big_kernel(
   vm_wait<0>();
   finish(nxt);
 
+  // Software pipeline (rows outer): the W2 fragments of a step and its first C sub-tile are read
+  // during the previous step, C sub-tile ms+1 under sub-tile ms's MFMAs; the barrier for the
+  // next block sits between the two MFMA halves of the last row sub-tile.
+  static_assert(MS % 2 == 0 && NS % 2 == 0, "pipeline shape");
+  v4u wq[NS][2];  // raw e4m3 W2 fragments of the step
+  v4u a[2][4];    // C fragments of two row sub-tiles
+  auto read_a = [&](uint32_t ab, int ms, v4u(&x)[4]) {
+    const int row = (wm * MS + ms) * 16 + r16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[c] = ds_read16(ab + row * ARow + 16 * ((4 * g + c) ^ (row & 15)));
+  };
+  auto read_head = [&](int d) {
+    const uint32_t bb = lds_addr(&bring[d][0]) + wn * NS * kWBlk;
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      wq[ns][0] = ds_read16(bb + ns * kWBlk + rd0);
+      wq[ns][1] = ds_read16(bb + ns * kWBlk + rd1);
+    }
+    read_a(lds_addr(&aring[d][0]), 0, a[0]);
+  };
+
   int slot = 0;
+  __builtin_amdgcn_s_barrier();  // block 0 has landed
+  read_head(0);
   for (;;) {
     const int it_nn = it_n + stride;
     meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
@@ -509,33 +587,17 @@ __global__ __launch_bounds__(320) void gemm2_big_kernel(
       for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = v4f{0.f, 0.f, 0.f, 0.f};
     int kb = 0;
     do {
-      const int d = slot;
-      __builtin_amdgcn_s_barrier();
+      const int d = slot, dn = slot + 1 == D ? 0 : slot + 1;
       const uint32_t ab = lds_addr(&aring[d][0]);
-      const uint32_t bb = lds_addr(&bring[d][0]) + wn * NS * kWBlk;
-      v4u wl[NS], wh[NS];
-#pragma unroll
-      for (int ns = 0; ns < NS; ++ns) {
-        wl[ns] = ds_read16(bb + ns * kWBlk + rd0);
-        wh[ns] = ds_read16(bb + ns * kWBlk + rd1);
-      }
-      auto read_a = [&](int ms, v4u (&a)[4]) {
-        const int row = (wm * MS + ms) * 16 + r16;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          a[c] = ds_read16(ab + row * ARow + 16 * ((4 * g + c) ^ (row & 15)));
-      };
-      v4u a[4];
-      read_a(0, a);
       const float sw = cur.sc.get(kb);
-      lds_wait_all();
+      lds_wait_all();  // the head fragments have landed
       v8bf bw[NS][4];
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns) {
-        lds_fence(wl[ns]);
-        lds_fence(wh[ns]);
-        const uint32_t wv[8] = {wl[ns][0], wl[ns][1], wl[ns][2], wl[ns][3],
-                                wh[ns][0], wh[ns][1], wh[ns][2], wh[ns][3]};
+        lds_fence(wq[ns][0]);
+        lds_fence(wq[ns][1]);
+        const uint32_t wv[8] = {wq[ns][0][0], wq[ns][0][1], wq[ns][0][2], wq[ns][0][3],
+                                wq[ns][1][0], wq[ns][1][1], wq[ns][1][2], wq[ns][1][3]};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           v2bf p0, p1, p2, p3;
@@ -545,28 +607,38 @@ __global__ __launch_bounds__(320) void gemm2_big_kernel(
         }
       }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) lds_fence(a[c]);
+      for (int c = 0; c < 4; ++c) lds_fence(a[0][c]);
+      auto mma = [&](int ms, int ns, const v4u(&x)[4]) {
+        v4f t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          t = mfma_bf16_16x16x32(bw[ns][c], __builtin_bit_cast(v8bf, x[c]), t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ms][ns][i] = fmaf(t[i], sw, acc[ms][ns][i]);
+      };
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) {
-        v8bf av[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) av[c] = __builtin_bit_cast(v8bf, a[c]);
-        if (ms + 1 < MS) read_a(ms + 1, a);
-#pragma unroll
-        for (int ns = 0; ns < NS; ++ns) {
-          v4f t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < 4; ++c) t = mfma_bf16_16x16x32(bw[ns][c], av[c], t);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[ms][ns][i] = fmaf(t[i], sw, acc[ms][ns][i]);
-        }
+        v4u(&x)[4] = a[ms & 1];
         if (ms + 1 < MS) {
+          read_a(ab, ms + 1, a[(ms + 1) & 1]);
+#pragma unroll
+          for (int ns = 0; ns < NS; ++ns) mma(ms, ns, x);
           lds_wait_all();
 #pragma unroll
-          for (int c = 0; c < 4; ++c) lds_fence(a[c]);
+          for (int c = 0; c < 4; ++c) lds_fence(a[(ms + 1) & 1][c]);
+        } else {
+          // last row sub-tile (a[1]; a[0] and wq are free for the next block's head)
+#pragma unroll
+          for (int ns = 0; ns < NS / 2; ++ns) mma(ms, ns, x);
+          // Block kb+1 has landed and slot d is no longer read. After the last block this
+          // barrier pairs with the producer's final one and the head read is unused.
+          __builtin_amdgcn_s_barrier();
+          read_head(dn);
+#pragma unroll
+          for (int ns = NS / 2; ns < NS; ++ns) mma(ms, ns, x);
         }
       }
-      slot = slot + 1 == D ? 0 : slot + 1;
+      slot = dn;
       ++kb;
     } while (kb < NKB);
     vm_wait<0>();
@@ -617,16 +689,28 @@ static inline long long big_tiles(int max_pairs, int bm, int E_l) {
 #define JG_B1_MS 4
 #endif
 #ifndef JG_B1_NS
-#define JG_B1_NS 4
+#define JG_B1_NS 2
+#endif
+#ifndef JG_B1_WM
+#define JG_B1_WM 2
+#endif
+#ifndef JG_B1_WN
+#define JG_B1_WN 4
 #endif
 #ifndef JG_B1_D
 #define JG_B1_D 3
 #endif
 #ifndef JG_B2_MS
-#define JG_B2_MS 4
+#define JG_B2_MS 2
 #endif
 #ifndef JG_B2_NS
 #define JG_B2_NS 4
+#endif
+#ifndef JG_B2_WM
+#define JG_B2_WM 4
+#endif
+#ifndef JG_B2_WN
+#define JG_B2_WN 2
 #endif
 #ifndef JG_B2_D
 #define JG_B2_D 3
@@ -636,10 +720,10 @@ hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint
                             const float* s13, const int32_t* counts, const int32_t* offsets,
                             const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                             int max_pairs, hipStream_t stream) {
-  constexpr int BN = 32 * JG_B1_NS;
+  constexpr int BN = 16 * JG_B1_NS * JG_B1_WN;
   if (I % BN != 0 || H / kBlock < JG_B1_D - 1) return hipErrorNotSupported;
-  const int grid = big_grid(big_tiles(max_pairs, 32 * JG_B1_MS, E_l) * (I / BN));
-  gemm1_big_kernel<JG_B1_MS, JG_B1_NS, JG_B1_D><<<grid, (kComputeWaves + 1) * kWave, 0, stream>>>(
+  const int grid = big_grid(big_tiles(max_pairs, 16 * JG_B1_MS * JG_B1_WM, E_l) * (I / BN));
+  gemm1_big_kernel<JG_B1_MS, JG_B1_NS, JG_B1_D, JG_B1_WM, JG_B1_WN><<<grid, (JG_B1_WM * JG_B1_WN + 1) * kWave, 0, stream>>>(
       hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs);
   return hipGetLastError();
 }
@@ -648,10 +732,10 @@ hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s
                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
                             float* partial, int H, int I, int E_l, int max_pairs,
                             hipStream_t stream) {
-  constexpr int BN = 32 * JG_B2_NS;
+  constexpr int BN = 16 * JG_B2_NS * JG_B2_WN;
   if (H % BN != 0 || I / kBlock < JG_B2_D - 1) return hipErrorNotSupported;
-  const int grid = big_grid(big_tiles(max_pairs, 32 * JG_B2_MS, E_l) * (H / BN));
-  gemm2_big_kernel<JG_B2_MS, JG_B2_NS, JG_B2_D><<<grid, (kComputeWaves + 1) * kWave, 0, stream>>>(
+  const int grid = big_grid(big_tiles(max_pairs, 16 * JG_B2_MS * JG_B2_WM, E_l) * (H / BN));
+  gemm2_big_kernel<JG_B2_MS, JG_B2_NS, JG_B2_D, JG_B2_WM, JG_B2_WN><<<grid, (JG_B2_WM * JG_B2_WN + 1) * kWave, 0, stream>>>(
       C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs);
   return hipGetLastError();
 }

@@ -149,7 +149,10 @@ __device__ __forceinline__ void lds_wait(v4u& x, v4u& y, v4u& z, v4u& w) {
 // Weight K-block image in LDS: 16 rows x 128 bytes, row n's 16-byte chunk c stored at position
 // c ^ ((n >> 1) & 7). A DMA instruction h (h = 0, 1) fills rows 8h..8h+7 with whole lines;
 // the MFMA operand read (lane = row n | group g, chunks 2g and 2g+1) is bank-conflict free.
-__device__ __forceinline__ int wblk_swz(int row) { return (row >> 1) & 7; }
+#ifndef JG_WBLK_SWZ
+#define JG_WBLK_SWZ 0
+#endif
+__device__ __forceinline__ int wblk_swz(int row) { return JG_WBLK_SWZ ? (row & 7) : ((row >> 1) & 7); }
 // Global byte offset, relative to row 0 of the block, that lane `lane` of DMA instruction h
 // fetches; `row_bytes` is the weight row pitch.
 __device__ __forceinline__ uint32_t wblk_dma_off(int lane, int h, int row_bytes) {
@@ -284,6 +287,63 @@ struct TileMap {
     }
     (void)lane;
     return e;
+  }
+};
+
+// The tile map of TileMap kept in LDS, for kernels whose register budget cannot hold the
+// per-lane arrays for the whole kernel (a spilled copy would be reloaded from scratch, and every
+// such reload waits for all outstanding vector-memory operations, LDS DMAs included).
+constexpr int kMaxLocalExperts = 4 * kWave;
+struct TileMapLds {
+  int32_t incl[kMaxLocalExperts], cnt[kMaxLocalExperts], seg[kMaxLocalExperts];
+
+  // Every wave calls this (all lanes); wave 0 stores the arrays. Returns the total tile count.
+  // The caller must __syncthreads() before the first find().
+  __device__ __forceinline__ int build(const int32_t* __restrict__ counts,
+                                       const int32_t* __restrict__ offsets, int n_experts, int bm,
+                                       bool store) {
+    TileMap tm;
+    tm.init(counts, offsets, n_experts, bm);
+    if (store) {
+      const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        incl[j * kWave + lane] = tm.incl[j];
+        cnt[j * kWave + lane] = tm.cnt[j];
+        seg[j * kWave + lane] = tm.seg[j];
+      }
+    }
+    return tm.total;
+  }
+
+  // Same contract as TileMap::find. Reads LDS with asm (lgkmcnt only).
+  template <int BM>
+  __device__ __forceinline__ int find(int slot, int n_experts, int& m0, int& count,
+                                      int& segment) const {
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t bi = lds_addr(incl) + 4 * lane, bc = lds_addr(cnt) + 4 * lane,
+                   bs = lds_addr(seg) + 4 * lane;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j * kWave >= n_experts) break;
+      float fi = ds_read4f(bi + 4 * kWave * j), fc = ds_read4f(bc + 4 * kWave * j),
+            fs = ds_read4f(bs + 4 * kWave * j);
+      lds_wait_all();
+      lds_fence(fi);
+      lds_fence(fc);
+      lds_fence(fs);
+      const int in = __float_as_int(fi), c = __float_as_int(fc);
+      const int nt = (c + BM - 1) / BM;
+      const unsigned long long m = __ballot(slot < in && slot >= in - nt);
+      if (m) {
+        const int src = __ffsll((long long)m) - 1;
+        m0 = (slot - __builtin_amdgcn_readlane(in - nt, src)) * BM;
+        count = __builtin_amdgcn_readlane(c, src);
+        segment = __builtin_amdgcn_readlane(__float_as_int(fs), src);
+        return j * kWave + src;
+      }
+    }
+    return 0;
   }
 };
 
