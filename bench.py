@@ -132,12 +132,28 @@ def measure(cfg, weights_dev, steps, warmup, dev, seed=None):
     return res, kw
 
 
+def measure_quant(T, H, steps, warmup, dev):
+    """The activation-quantisation kernel on a bf16 [T, H] batch already in HBM: algorithmic bytes
+    = bf16 read + e4m3 write + fp32 scales (2 + 1 + 4/128 bytes per element)."""
+    from justgoal_amd.moe import quantize_activations
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(2)).bfloat16().to(dev)
+    q = torch.empty((T, H), dtype=torch.float8_e4m3fn, device=dev)
+    sc = torch.empty((H // BLOCK, T), dtype=torch.float32, device=dev)
+    ms = time_calls(lambda: quantize_activations(x, q, sc), steps, warmup, dev)
+    nbytes = T * H * 3 + T * (H // BLOCK) * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(tokens=T, hidden=H, ms_per_call=ms, bytes=nbytes, gb_s=gbs,
+                hbm_frac=gbs / PEAK_HBM_GBS)
+
+
 def gemm1_kernel_name(cfg):
     """The GEMM1+SwiGLU kernel family the library picks for this shape: the shape-only rule of
-    justgoal_amd/csrc/moe_gemm.hip (expected pairs per expert T*top_k/E <= 16 -> streaming)."""
+    justgoal_amd/csrc/moe_gemm.hip (expected pairs per expert T*top_k/E: <= 16 streaming,
+    >= 64 large tiles, else LDS tiles)."""
     g = cfg.geom
-    return ("gemm1_stream_kernel" if cfg.tokens * g.top_k // g.num_experts <= 16
-            else "gemm1_tile_kernel")
+    rows = cfg.tokens * g.top_k // g.num_experts
+    return ("gemm1_stream_kernel" if rows <= 16 else
+            "gemm1_tile_kernel" if rows < 64 else "gemm1_big_kernel")
 
 
 def load_traffic(name):
@@ -222,6 +238,10 @@ def main():
             f"{r['gb_s']:.0f} GB/s, stages {r['stage_ms']}")
         secondary.append(r)
         del w
+    quant = [measure_quant(T, cfg.geom.hidden, args.steps, args.warmup, dev) for T in (4096, 64)]
+    for r in quant:
+        log(f"[bench] activation quant T={r['tokens']}: {r['ms_per_call'] * 1e3:.1f} us, "
+            f"{r['gb_s']:.0f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU oracle")
@@ -250,6 +270,7 @@ def main():
         "cpu_baseline": cpu,
         "headline": head,
         "secondary": secondary,
+        "activation_quant": quant,
     }
     print(json.dumps(out), flush=True)
 

@@ -118,6 +118,17 @@ int moe_workspace_layout(const moe_geometry* geom, int T, int64_t* offsets);
 #define MOE_NUM_STAGES 5
 int moe_set_stage_events(void* const* events, int n);
 
+/*
+ * Activation quantisation, the step that produces `hs` / `hs_scale` for moe_run:
+ * x bf16 [T, H] -> q e4m3fn [T, H], scale fp32 [H/128, T]. Per 1x128 block of a row,
+ * scale = amax / 448 (0 for an all-zero block) and q = e4m3(clamp(x / s, -448, 448)) with
+ * s = scale (1 when scale is 0), round to nearest even. H must be a multiple of 128.
+ * Replaces: the per-row block quantisation the reference applies before its fp8 GEMM2
+ *   (goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:151-156, same rule and constants)
+ * and the hidden-state quantisation its harness performs to build `hidden_states_scale`.
+ */
+int moe_quantize_activations(const void* x, int T, int H, void* q, void* scale, void* stream);
+
 /* Static description of a return code. */
 const char* moe_error_string(int rc);
 

@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libjustgoal_moe.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["moe_api.hip", "moe_routing.hip", "moe_gemm.hip", "moe_stream.hip", "moe_tile.hip", "moe_big.hip"]
+SOURCES = ["moe_api.hip", "moe_routing.hip", "moe_gemm.hip", "moe_stream.hip", "moe_tile.hip", "moe_big.hip", "moe_quant.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

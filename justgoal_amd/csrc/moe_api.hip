@@ -231,6 +231,17 @@ int moe_run(const void* logits, const void* bias, const void* hs, const void* hs
                     out, workspace, T, stream);
 }
 
+int moe_quantize_activations(const void* x, int T, int H, void* q, void* scale, void* stream) {
+  if (T < 0 || H <= 0 || H % 128 != 0) return MOE_ERR_INVALID_ARG;
+  if (T == 0) return MOE_OK;
+  if (!x || !q || !scale) return MOE_ERR_INVALID_ARG;
+  const int rc = check_device();
+  if (rc != MOE_OK) return rc;
+  JG_TRY(jgmoe::launch_quantize_activations((const uint16_t*)x, T, H, (uint8_t*)q, (float*)scale,
+                                            (hipStream_t)stream));
+  return MOE_OK;
+}
+
 const char* moe_error_string(int rc) {
   switch (rc) {
     case MOE_OK: return "success";

@@ -72,4 +72,9 @@ hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* 
 hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,
                           uint16_t* out, hipStream_t stream);
 
+// Activation quantisation: bf16 [T, H] -> e4m3 [T, H] and fp32 scales [H/128, T] (1x128 blocks,
+// scale = amax / 448). H must be a multiple of 128.
+hipError_t launch_quantize_activations(const uint16_t* x, int T, int H, uint8_t* q, float* scale,
+                                       hipStream_t stream);
+
 }  // namespace jgmoe

@@ -1,0 +1,90 @@
+// Activation quantisation: bf16 hidden states -> e4m3 codes with per-token 1x128 block scales,
+// the producer of the operator's `hidden_states` / `hidden_states_scale` inputs.
+//
+// Rule (the reference applies it to its SwiGLU output before GEMM2,
+// goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:151-156): per 128-column block of a row,
+// amax = max |x|, scale = amax / 448 (0 for an all-zero block), codes = e4m3(clamp(x / s, -448,
+// 448)) with s = scale, or 1 when scale is 0; fp32 arithmetic, correctly rounded division,
+// round-to-nearest-even conversion. Scales are stored transposed, [H/128, T].
+//
+// HBM-bound (3 bytes per element plus 4 per 128 elements). A workgroup owns 16 tokens x 512
+// columns: each wave quantises one token's 512 columns per pass (lane = 8 columns of one block;
+// the block amax is a 16-lane xor reduction), so loads are 1 KiB and code stores 512 B per wave
+// instruction; the workgroup's 64 scales leave through LDS as four 64-byte rows of the
+// transposed scale matrix.
+#include "moe_device.h"
+#include "moe_kernels.h"
+
+namespace jgmoe {
+
+namespace {
+
+constexpr int kQTok = 16;    // tokens per workgroup
+constexpr int kQBlk = 4;     // 128-column blocks per workgroup (512 columns)
+constexpr int kQWaves = 4;
+
+// Four fp32 -> four e4m3 bytes (OCP e4m3fn on gfx950), round to nearest even. Inputs are
+// already clamped to [-448, 448], so saturation never applies.
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
+  int v = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, v, true);
+  return (uint32_t)v;
+}
+
+__global__ __launch_bounds__(kQWaves * kWave) void quant_act_kernel(
+    const uint16_t* __restrict__ x, int T, int H, uint8_t* __restrict__ q,
+    float* __restrict__ scale) {
+  __shared__ float sc[kQBlk][kQTok];
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
+  const int NB = H / kBlock;
+  const int t0 = blockIdx.x * kQTok, b0 = blockIdx.y * kQBlk;
+  const int blk = b0 + (lane >> 4);  // this lane's 128-column block
+  const bool active = blk < NB;
+  const int col = blk * kBlock + 8 * (lane & 15);
+  for (int j = w; j < kQTok; j += kQWaves) {
+    const int t = t0 + j;  // wave-uniform
+    float v[8];
+    float amax = 0.f;
+    const bool live = t < T && active;  // uniform over each 16-lane block group
+    if (live) {
+      const uint4 raw = *(const uint4*)(x + (size_t)t * H + col);
+      const uint32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(r[i] << 16);
+        v[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float cs = __fdiv_rn(amax, 448.0f);
+    const float div = cs > 0.f ? cs : 1.0f;
+    if (live) {
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(__fdiv_rn(v[i], div), -448.0f), 448.0f);
+      *(uint2*)(q + (size_t)t * H + col) =
+          uint2{f32x4_to_e4m3(y[0], y[1], y[2], y[3]), f32x4_to_e4m3(y[4], y[5], y[6], y[7])};
+    }
+    if ((lane & 15) == 0) sc[lane >> 4][j] = cs;
+  }
+  __syncthreads();
+  if (w == 0) {
+    const int b = b0 + (lane >> 4), t = t0 + (lane & 15);
+    if (b < NB && t < T) scale[(size_t)b * T + t] = sc[lane >> 4][lane & 15];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_quantize_activations(const uint16_t* x, int T, int H, uint8_t* q, float* scale,
+                                       hipStream_t stream) {
+  const int NB = H / kBlock;
+  const dim3 grid((T + kQTok - 1) / kQTok, (NB + kQBlk - 1) / kQBlk);
+  quant_act_kernel<<<grid, kQWaves * kWave, 0, stream>>>(x, T, H, q, scale);
+  return hipGetLastError();
+}
+
+}  // namespace jgmoe

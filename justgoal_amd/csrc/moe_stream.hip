@@ -26,6 +26,13 @@
 #include "moe_device.h"
 #include "moe_kernels.h"
 
+#ifndef JG_G2S_BOUNDED
+#define JG_G2S_BOUNDED 0
+#endif
+#ifndef JG_ABL_NOC
+#define JG_ABL_NOC 0
+#endif
+
 namespace jgmoe {
 
 namespace {
@@ -241,6 +248,8 @@ struct G2Item {
   LaneScales sc;         // weight scales of the 128-row block holding h0, per K block
   uint32_t coff[MT];     // per lane: byte offset of C[pair][32 g]
   float wgt[MT];         // routing weight of the lane's pair
+  const uint16_t* cbase; // C row of the tile's first pair
+  uint32_t crec;         // bytes of C from cbase to the segment's end
   int m0, cnt, seg, h0;
 };
 
@@ -284,9 +293,12 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
     for (int mt = 0; mt < MT; ++mt) {
       const int r = x.m0 + mt * 16 + r16;
       const int p = x.seg + (r < x.cnt ? r : x.cnt - 1);
-      x.coff[mt] = ((uint32_t)p * I + 32 * g) * 2;
+      x.coff[mt] = JG_G2S_BOUNDED ? ((uint32_t)(mt * 16 + r16) * I + 32 * g) * 2
+                                  : ((uint32_t)p * I + 32 * g) * 2;
       x.wgt[mt] = sorted_w[p];
     }
+    x.cbase = uniform(C + (size_t)(x.seg + x.m0) * I);
+    x.crec = uniform((uint32_t)(x.cnt - x.m0) * I * 2);
   };
 
   G2Item<MT> cur, nxt, nn;
@@ -296,11 +308,16 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
 
   G2Slot<MT> sl[D];
   auto issue = [&](bool second, int kbi, G2Slot<MT>& s, int d) {
+    const __amdgpu_buffer_rsrc_t cr =
+        JG_G2S_BOUNDED ? make_rsrc(uniform(second ? nxt.cbase : cur.cbase),
+                                   uniform(second ? nxt.crec : cur.crec))
+                       : cres;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const uint32_t co = second ? nxt.coff[mt] : cur.coff[mt];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) s.a[mt][c] = buf_load16(cres, co, 2 * (kbi * kBlock + 8 * c));
+      for (int c = 0; c < 4; ++c)
+        s.a[mt][c] = JG_ABL_NOC ? uint4{0, 0, 0, 0} : buf_load16(cr, co, 2 * (kbi * kBlock + 8 * c));
     }
     const __amdgpu_buffer_rsrc_t wres =
         make_rsrc(uniform(second ? nxt.wbase : cur.wbase), (uint32_t)H * I);

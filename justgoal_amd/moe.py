@@ -181,6 +181,37 @@ def route(routing_logits, routing_bias, local_expert_offset, routed_scaling_fact
     return workspace_views(geom, T, ws)
 
 
+@torch.no_grad()
+def quantize_activations(hidden_states, out=None, scale_out=None):
+    """bf16 [T, H] -> (float8_e4m3fn [T, H], fp32 scales [H/128, T]): the per-token 1x128 block
+    quantisation that produces ``hidden_states`` / ``hidden_states_scale`` for ``run``
+    (rule of goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:151-156: scale = amax / 448).
+    Runs the HIP kernel behind ``moe_quantize_activations`` on the current stream."""
+    x = hidden_states
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise TypeError("hidden_states must be a bf16 [T, H] tensor")
+    x = x.contiguous()
+    T, H = x.shape
+    if H % 128 != 0:
+        raise ValueError("H must be a multiple of 128")
+    dev = x.device
+    if dev.type != "cuda":
+        raise ValueError("hidden_states must be on a GPU")
+    if out is None:
+        out = torch.empty((T, H), dtype=F8, device=dev)
+    if scale_out is None:
+        scale_out = torch.empty((H // 128, T), dtype=torch.float32, device=dev)
+    if (out.dtype != F8 or tuple(out.shape) != (T, H) or not out.is_contiguous()
+            or scale_out.dtype != torch.float32 or tuple(scale_out.shape) != (H // 128, T)
+            or not scale_out.is_contiguous()):
+        raise ValueError("out must be e4m3fn [T, H] and scale_out fp32 [H/128, T], contiguous")
+    rc = _lib.lib().moe_quantize_activations(x.data_ptr(), T, H, out.data_ptr(),
+                                             scale_out.data_ptr(),
+                                             torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check(rc, "moe_quantize_activations")
+    return out, scale_out
+
+
 def workspace_views(geom: Geometry, T: int, ws: torch.Tensor) -> dict:
     """Typed views of the workspace regions (the layout moe_workspace_layout reports)."""
     L = _lib.workspace_layout(geom, T)

@@ -149,6 +149,24 @@ def permute(topk_idx, topk_w, local_offset: int, E_local: int):
                 pair_of=pair_of)
 
 
+def quantize_activations(x: torch.Tensor):
+    """bf16/fp32 [T, H] -> (e4m3fn [T, H], fp32 scales [H/128, T]), per 1x128 row block.
+
+    The reference's block-quantisation rule (goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/
+    main.py:151-156): amax over the block, scale = amax / 448 (stored as is, so 0 for an all-zero
+    block), divisor = scale or 1 when scale is 0, codes = clamp(x / divisor, -448, 448) rounded to
+    e4m3 (nearest even). fp32 throughout; torch's CPU division is IEEE and its float8_e4m3fn cast
+    rounds to nearest even (pinned against a table-driven encoder in tests/test_oracle.py).
+    """
+    T, H = x.shape
+    xb = x.float().reshape(T, H // 128, 128)
+    amax = xb.abs().amax(dim=2)
+    scale = amax / 448.0
+    div = torch.where(scale > 0, scale, torch.ones_like(scale))
+    q = (xb / div[:, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).reshape(T, H)
+    return q, scale.t().contiguous()
+
+
 def dequant_blocks(q: torch.Tensor, scale: torch.Tensor, block: int = 128) -> torch.Tensor:
     """fp8 [..., R, C] with fp32 block scales [..., R/block, C/block] -> fp32 (D1)."""
     s = scale.float().repeat_interleave(block, dim=-2).repeat_interleave(block, dim=-1)
