@@ -11,6 +11,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB_NAME = "libjustgoal_moe.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["moe_api.hip", "moe_routing.hip", "moe_gemm.hip", "moe_stream.hip", "moe_tile.hip", "moe_big.hip", "moe_quant.hip"]
@@ -36,7 +37,8 @@ def build(verbose: bool = False, out: str = LIB_PATH, defines=(), extra_flags=()
     the default build uses none."""
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
     tmp = out + f".{os.getpid()}.tmp"
-    cmd = [HIPCC, *FLAGS, *extra_flags, *[f"-D{d}" for d in defines], "-o", tmp, *srcs]
+    cmd = [HIPCC, *FLAGS, f"-I{INCLUDE}", *extra_flags, *[f"-D{d}" for d in defines], "-o", tmp,
+           *srcs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

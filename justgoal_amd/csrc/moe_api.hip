@@ -6,7 +6,7 @@
 #include <mutex>
 #include <string>
 
-#include "../../include/justgoal_moe.h"
+#include "justgoal_moe.h"
 #include "moe_kernels.h"
 
 namespace {

@@ -20,6 +20,9 @@
 #include "moe_device.h"
 #include "moe_kernels.h"
 
+#ifndef JG_XCD_MAP
+#define JG_XCD_MAP 0
+#endif
 #ifndef JG_ABL_NODMA
 #define JG_ABL_NODMA 0
 #endif
@@ -33,6 +36,20 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kWBlk = 16 * kBlock;  // 16 rows x 128 bytes
+
+// A buffer offset past every buffer these kernels address (all are < 2 GiB; the launchers check).
+constexpr uint32_t kOutOfRange = 0x7ffffff0u;
+
+// Optional (JG_XCD_MAP=1; measured mixed: Qwen3 GEMM1 -13%, DS T=4096 GEMM1 +15%, so off).
+// Workgroups are dispatched to the 8 XCDs round-robin (workgroup b runs on XCD b % 8), and the
+// persistent loop hands workgroup b the items b, b + grid, ... (grid a multiple of 8). This
+// bijection on [0, items) gives XCD x a contiguous run of the tile-major item list instead of
+// every 8th item, so the column items of one M-tile (sharing its activation rows) and the M-tiles
+// of one expert (sharing its weights) meet in the same L2.
+__device__ __forceinline__ int xcd_item(int i, int items) {
+  const int x = i & 7, q = items >> 3, r = items & 7;
+  return x * q + (x < r ? x : r) + (i >> 3);
+}
 
 constexpr int vm_depth(int n) { return n > 63 ? 63 : n < 0 ? 0 : n; }
 
@@ -88,7 +105,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
   const int stride = gridDim.x;
 
   auto scalars = [&](int item, B1Scalars& x) {
-    item = uniform(item);
+    item = uniform(JG_XCD_MAP ? xcd_item(item, items) : item);
     const int tile = item / NNT, nt = item % NNT;
     x.e = uniform(tml.template find<BM>(tile, E_l, x.m0, x.cnt, x.seg));
     x.m0 = uniform(x.m0);
@@ -130,11 +147,17 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
       lds_wait_all();
 #pragma unroll
       for (int j = 0; j < AI + SI; ++j) lds_fence(t[j]);
+      // Rows past the segment get an offset beyond both buffers: their DMAs fetch nothing (the
+      // LDS rows they would fill only feed output rows that are never stored).
+      const int valid = x.s.cnt - x.s.m0;
 #pragma unroll
       for (int j = 0; j < AI; ++j)
-        x.aoff[j] = __float_as_uint(t[j]) * H + 16 * ((lane & 7) ^ wblk_swz(8 * j + (lane >> 3)));
+        x.aoff[j] = 8 * j + (lane >> 3) < valid
+                        ? __float_as_uint(t[j]) * H + 16 * ((lane & 7) ^ wblk_swz(8 * j + (lane >> 3)))
+                        : kOutOfRange;
 #pragma unroll
-      for (int k = 0; k < SI; ++k) x.saoff[k] = __float_as_uint(t[AI + k]) * 4;
+      for (int k = 0; k < SI; ++k)
+        x.saoff[k] = k * kWave + lane < valid ? __float_as_uint(t[AI + k]) * 4 : kOutOfRange;
     };
     P cur, nxt, nn;
     meta(it, cur);
@@ -172,23 +195,24 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
     for (;;) {
       const int it_nn = it_n + stride;
       meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
+      // Refills come from the current item until its last block is issued, then from the next
+      // one; two loops (not a per-step select) so the current item's offsets are dead in the
+      // second and only two items' offsets are ever live.
       int kb = 0;
-      do {
+      for (; kb + D - 1 < NKB; ++kb) {
         vm_wait<vm_depth((D - 2) * OPS)>();  // the DMAs of block kb have landed
         __builtin_amdgcn_s_barrier();
-        const int kn = kb + D - 1;
-        const bool second = kn >= NKB;
-        // a uniform branch, so the per-lane offsets are not selected op by op
-        if (!JG_ABL_NODMA) {
-          if (second)
-            issue(nxt, kn - NKB, slot == 0 ? D - 1 : slot - 1);
-          else
-            issue(cur, kn, slot == 0 ? D - 1 : slot - 1);
-        }
+        if (!JG_ABL_NODMA) issue(cur, kb + D - 1, slot == 0 ? D - 1 : slot - 1);
         __builtin_amdgcn_sched_barrier(0);
         slot = slot + 1 == D ? 0 : slot + 1;
-        ++kb;
-      } while (kb < NKB);
+      }
+      for (; kb < NKB; ++kb) {
+        vm_wait<vm_depth((D - 2) * OPS)>();
+        __builtin_amdgcn_s_barrier();
+        if (!JG_ABL_NODMA) issue(nxt, kb + D - 1 - NKB, slot == 0 ? D - 1 : slot - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        slot = slot + 1 == D ? 0 : slot + 1;
+      }
       vm_wait<vm_depth((D - 1) * OPS)>();  // the token-list DMAs of the next-but-one tile
       finish(nn);
       if (it_n >= items) break;
@@ -434,7 +458,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
   const int stride = gridDim.x;
 
   auto scalars = [&](int item, B2Scalars& x) {
-    item = uniform(item);
+    item = uniform(JG_XCD_MAP ? xcd_item(item, items) : item);
     const int tile = item / NNT, nt = item % NNT;
     x.e = uniform(tml.template find<BM>(tile, E_l, x.m0, x.cnt, x.seg));
     x.m0 = uniform(x.m0);
@@ -721,7 +745,8 @@ hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint
                             const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                             int max_pairs, hipStream_t stream) {
   constexpr int BN = 16 * JG_B1_NS * JG_B1_WN;
-  if (I % BN != 0 || H / kBlock < JG_B1_D - 1) return hipErrorNotSupported;
+  if (I % BN != 0 || H / kBlock < JG_B1_D - 1 || (int64_t)T * H >= kOutOfRange)
+    return hipErrorNotSupported;
   const int grid = big_grid(big_tiles(max_pairs, 16 * JG_B1_MS * JG_B1_WM, E_l) * (I / BN));
   gemm1_big_kernel<JG_B1_MS, JG_B1_NS, JG_B1_D, JG_B1_WM, JG_B1_WN><<<grid, (JG_B1_WM * JG_B1_WN + 1) * kWave, 0, stream>>>(
       hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs);
