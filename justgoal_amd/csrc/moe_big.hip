@@ -40,7 +40,7 @@ constexpr int kWBlk = 16 * kBlock;  // 16 rows x 128 bytes
 // A buffer offset past every buffer these kernels address (all are < 2 GiB; the launchers check).
 constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 
-// Optional (JG_XCD_MAP=1; measured mixed: Qwen3 GEMM1 -13%, DS T=4096 GEMM1 +15%, so off).
+// Optional (JG_XCD_MAP=1; measured mixed: Qwen3 GEMM1 13% faster, DS-V3 T=4096 GEMM1 15% slower, so off).
 // Workgroups are dispatched to the 8 XCDs round-robin (workgroup b runs on XCD b % 8), and the
 // persistent loop hands workgroup b the items b, b + grid, ... (grid a multiple of 8). This
 // bijection on [0, items) gives XCD x a contiguous run of the tile-major item list instead of
