@@ -1,7 +1,7 @@
 // Routing and token-permute kernels.
 //
-// route_kernel: one wave64 per token (16 tokens per workgroup), each lane owning VPL = E/64
-//   consecutive experts.
+// route_kernel: one wave64 per token (4 tokens per workgroup up to T = 256, 16 above), each
+//   lane owning VPL = E/64 consecutive experts.
 //   DeepSeek no-aux routing (reference semantics: goal_full_shape/fable-5.1/moe_fp8_fwd/MOEDIR/
 //   moe_common.cuh:271-365, kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t14107/
 //   moe_kernel.cu:482-600): sigmoid, + bias, group score = sum of the group's top two, keep
@@ -25,7 +25,14 @@ namespace jgmoe {
 
 namespace {
 
-constexpr int kRouteWaves = 16;          // tokens per routing workgroup (one wave each)
+constexpr int kRouteWaves = 16;          // most tokens per routing workgroup (one wave each)
+// Routing is VALU-throughput-bound (fp64 sigmoid, DPP top-k chains): small batches use 4-token
+// workgroups so their tokens spread over more CUs; larger ones keep 16 per workgroup so the
+// permute kernel has fewer count rows to sum.
+constexpr int kRouteSmallT = 256, kRouteWavesSmall = 4;
+__host__ __device__ __forceinline__ int route_tokens_per_group(int T) {
+  return T <= kRouteSmallT ? kRouteWavesSmall : kRouteWaves;
+}
 constexpr int kPlaceTokens = 64;         // tokens per permute workgroup (one bitmask word)
 constexpr int kMaxLocal = 256;           // local experts supported by the count / scan stages
 
@@ -277,11 +284,12 @@ __global__ __launch_bounds__(1024) void route_kernel(
     int topk_group, int top_k, float rsf, int local_offset, int E_l, int32_t* __restrict__ topk_idx,
     float* __restrict__ topk_w, int32_t* __restrict__ hist) {
   constexpr int E = VPL * kWave;
-  __shared__ TokenPairs tp;  // rows 0..15 used
+  __shared__ TokenPairs tp;  // rows 0..tpw-1 used
   __shared__ ExpertMasks masks;
   __shared__ int cnt[kMaxLocal];
   const int lane = threadIdx.x & (kWave - 1), wave = wave_id();
-  const int t0 = blockIdx.x * kRouteWaves;
+  const int tpw = blockDim.x / kWave;  // tokens of this workgroup
+  const int t0 = blockIdx.x * tpw;
   const int t = t0 + wave;
 
   int le = -1;
@@ -306,7 +314,7 @@ __global__ __launch_bounds__(1024) void route_kernel(
     tp.w[wave][lane] = w;
   }
   __syncthreads();
-  build_masks(tp, kRouteWaves, top_k, E_l, masks, cnt);
+  build_masks(tp, tpw, top_k, E_l, masks, cnt);
   for (int e = threadIdx.x; e < E_l; e += blockDim.x) hist[(size_t)blockIdx.x * E_l + e] = cnt[e];
 }
 
@@ -323,7 +331,7 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __shared__ int before[kMaxLocal];
   __shared__ int off[kMaxLocal + 1];
   const int t0 = blockIdx.x * kPlaceTokens;
-  const int row0 = t0 / kRouteWaves;  // first count row of this chunk
+  const int row0 = t0 / route_tokens_per_group(T);  // first count row of this chunk
   // Column sums of the count table: thread (e, slice) adds every n_slices-th row of column e;
   // loads are issued eight at a time so they overlap.
   const int n_slices = max(1, (int)blockDim.x / E_l);
@@ -377,14 +385,17 @@ __global__ __launch_bounds__(256) void permute_kernel(
   place_from_masks(tp, masks, n, t0, T, K, before, sorted_tok, sorted_w, pair_of);
 }
 
-int route_chunks(int T) { return (T + kRouteWaves - 1) / kRouteWaves; }
+int route_chunks(int T) {
+  const int tpw = route_tokens_per_group(T);
+  return (T + tpw - 1) / tpw;
+}
 
 hipError_t launch_route(const float* logits, const uint16_t* bias, int T, int E, int n_group,
                         int topk_group, int top_k, int method, float rsf, int local_offset,
                         int E_l, int32_t* topk_idx, float* topk_w, int32_t* hist,
                         hipStream_t stream) {
   if (E_l > kMaxLocal || top_k > kMaxTopK) return hipErrorInvalidValue;
-  const dim3 grid(route_chunks(T)), block(kRouteWaves * kWave);
+  const dim3 grid(route_chunks(T)), block(route_tokens_per_group(T) * kWave);
 #define JG_ROUTE(VPL)                                                                        \
   if (E == VPL * kWave) {                                                                    \
     if (method == ROUTING_DS)                                                                \
