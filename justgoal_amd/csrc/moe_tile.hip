@@ -531,6 +531,7 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
                              int max_pairs, int mt, hipStream_t stream) {
 #define JG_G1T(MT, D)                                                                           \
   {                                                                                             \
+    if (H / kBlock < (D) - 1) return hipErrorNotSupported; /* lead must stay within one item */ \
     constexpr int lds = kWaves * D * 2 * kWBlk + D * 16 * MT * kBlock + D * 16 * MT * 4 +      \
                         kWaves * (MT / 2 + 5) * kWave * 4;                                       \
     const int grid =                                                                            \
@@ -551,6 +552,7 @@ hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* 
                              int max_pairs, int mt, hipStream_t stream) {
 #define JG_G2T(MT, NW, D)                                                                        \
   {                                                                                              \
+    if (I / kBlock < (D) - 1) return hipErrorNotSupported; /* lead must stay within one item */  \
     constexpr int lds = kWaves * D * NW * kWBlk + D * 16 * MT * 2 * kBlock +                     \
                         kWaves * (MT + 2 * NW) * kWave * 4;                                      \
     const int grid = tile_grid(tile_groups_per_cu(lds),                                          \

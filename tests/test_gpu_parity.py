@@ -200,3 +200,38 @@ def test_dps_output(gpu):
     res = run(**kw, output=dst, geometry=MINI_DS)
     assert res.data_ptr() == dst.data_ptr()
     assert torch.equal(dst, ref)
+
+
+# Routing workgroups hold 4 tokens up to T=256 and 16 above: both sides of the switch and ragged
+# counts around it (permute then sums 64 or 17 count rows).
+@pytest.mark.parametrize("T", [4, 255, 256, 257, 513])
+def test_route_group_boundary(gpu, T):
+    check_case(MINI_DS, T, gpu, seed=T + 1)
+
+
+# The maximum of 256 local experts (all global experts local) through the large-tile kernels:
+# T * top_k / E = 64 selects them, and the tile map spans all four 64-expert chunks.
+ALL_LOCAL = Geometry(256, 128, 256, 256, 8, 8, 4, ROUTING_DS, "all-local")
+
+
+def test_all_local_experts_large_tiles(gpu):
+    check_case(ALL_LOCAL, 2048, gpu, seed=9, tokens_checked=200)
+
+
+# Softmax routing on an EP rank that holds a subset of the experts, and fewer than 8 picks.
+SOFTMAX_EP = Geometry(256, 256, 128, 32, 6, 1, 1, ROUTING_SOFTMAX, "softmax-ep-top6")
+
+
+@pytest.mark.parametrize("off", [0, 96])
+def test_softmax_ep_subset_top6(gpu, off):
+    check_case(SOFTMAX_EP, 333, gpu, seed=off + 3, local_offset=off)
+
+
+# One K block per GEMM (H = I = 128): shorter than the two-block prefetch lead of the LDS-tile
+# and large-tile kernels, which then hand the shape to the streaming kernels (ring depth 1).
+SHORT_K = Geometry(128, 128, 64, 16, 4, 4, 2, ROUTING_DS, "short-K")
+
+
+@pytest.mark.parametrize("T", [40, 300])
+def test_single_k_block(gpu, T):
+    check_case(SHORT_K, T, gpu, seed=T + 5)
