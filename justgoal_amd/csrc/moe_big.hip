@@ -381,6 +381,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
           // barrier pairs with the producer's final one and the head read is unused.
           __builtin_amdgcn_s_barrier();
           read_head(dn);
+          __builtin_amdgcn_sched_barrier(0);  // keep the head reads ahead of the last MFMAs
 #pragma unroll
           for (int ms = 2; ms < MS; ++ms) mma(ms, ns, b);
         }
@@ -657,7 +658,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
           // Block kb+1 has landed and slot d is no longer read. After the last block this
           // barrier pairs with the producer's final one and the head read is unused.
           __builtin_amdgcn_s_barrier();
-          read_head(dn);
+          read_head(dn);  // (pinning these ahead of the MFMAs, as in GEMM1, measured slower here)
 #pragma unroll
           for (int ns = NS / 2; ns < NS; ++ns) mma(ms, ns, x);
         }
