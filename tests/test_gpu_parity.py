@@ -235,3 +235,44 @@ SHORT_K = Geometry(128, 128, 64, 16, 4, 4, 2, ROUTING_DS, "short-K")
 @pytest.mark.parametrize("T", [40, 300])
 def test_single_k_block(gpu, T):
     check_case(SHORT_K, T, gpu, seed=T + 5)
+
+
+def random_geometries(n, seed=2024, large=False):
+    """Seeded valid geometries spanning every kernel family (rows_hint = T*top_k/E from 0 to ~80),
+    both routing methods, partial EP ranks and odd token counts. Sizes stay small enough for the
+    CPU oracle to check every token."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        H = 128 * int(rng.integers(1, 7))
+        I = 128 * int(rng.integers(1, 5))
+        E = 64 if large else int(rng.choice([64, 128, 256, 512]))
+        El = int(rng.integers(1, min(E, 256) + 1))
+        if El * H * 3 * I > 40_000_000:
+            continue
+        K = int(rng.integers(6, 9)) if large else int(rng.integers(1, 9))
+        if rng.random() < 0.6:
+            method = ROUTING_DS
+            vpl = E // 64
+            gs = int(rng.choice([vpl << j for j in range(7) if (vpl << j) <= E]))
+            ng = E // gs
+            kg = int(rng.integers(1, ng + 1))
+            if K > kg * gs:
+                continue
+        else:
+            method, ng, kg = ROUTING_SOFTMAX, 1, 1
+        T = int(rng.integers(600, 1400)) if large else int(rng.integers(1, 700))
+        off = int(rng.integers(0, E - El + 1)) if rng.random() < 0.7 else 0
+        bias = bool(rng.random() < 0.8)
+        out.append((Geometry(H, I, E, El, K, ng, kg, method, f"rand{len(out)}"), T, off, bias))
+    return out
+
+
+@pytest.mark.parametrize("case", random_geometries(24) + random_geometries(8, 77, large=True),
+                         ids=lambda c: f"{c[0].name}-T{c[1]}")
+def test_random_geometries(gpu, case):
+    geom, T, off, bias = case
+    say(f"  geometry H={geom.hidden} I={geom.intermediate} E={geom.num_experts} "
+        f"El={geom.local_experts} K={geom.top_k} groups={geom.n_group}/{geom.topk_group} "
+        f"method={geom.routing_method} rows_hint={T * geom.top_k // geom.num_experts}")
+    check_case(geom, T, gpu, seed=T, local_offset=off, bias=bias)
