@@ -8,9 +8,10 @@ dependencies, destination_passing_style, binding) / sources / description, next 
 files it lists. ``main.py`` is ``solution_main.py`` of this package; the HIP sources and the C
 header ship beside it.
 
-``python -m justgoal_amd.solution DEST [--embed] [--with-lib]``: ``--embed`` also stores each
-source's text in solution.json (the opus-4.8 form); ``--with-lib`` ships the built
-libjustgoal_moe.so so the entry point loads it instead of compiling.
+``python -m justgoal_amd.solution DEST [--embed] [--with-lib] [--dps]``: ``--embed`` also stores
+each source's text in solution.json (the opus-4.8 form); ``--with-lib`` ships the built
+libjustgoal_moe.so so the entry point loads it instead of compiling; ``--dps`` declares the
+destination-passing form (the harness passes ``output`` as an eleventh argument, t901/main.py).
 """
 from __future__ import annotations
 
@@ -35,7 +36,8 @@ def source_files():
     return files
 
 
-def write_solution(dest: str, embed: bool = False, with_lib: bool = False) -> str:
+def write_solution(dest: str, embed: bool = False, with_lib: bool = False,
+                   dps: bool = False) -> str:
     """Writes the solution directory; returns the path of solution.json."""
     os.makedirs(dest, exist_ok=True)
     sources = []
@@ -60,7 +62,7 @@ def write_solution(dest: str, embed: bool = False, with_lib: bool = False) -> st
             "target_hardware": ["AMD MI355X"],
             "entry_point": "main.py::run",
             "dependencies": [],
-            "destination_passing_style": False,
+            "destination_passing_style": dps,
             "binding": None,
         },
         "sources": sources,
@@ -79,8 +81,9 @@ def main():
     ap.add_argument("dest")
     ap.add_argument("--embed", action="store_true")
     ap.add_argument("--with-lib", action="store_true")
+    ap.add_argument("--dps", action="store_true")
     a = ap.parse_args()
-    print(write_solution(a.dest, embed=a.embed, with_lib=a.with_lib))
+    print(write_solution(a.dest, embed=a.embed, with_lib=a.with_lib, dps=a.dps))
 
 
 if __name__ == "__main__":

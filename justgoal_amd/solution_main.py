@@ -1,8 +1,10 @@
 """FP8 block-scale MoE (DeepSeek-V3 no-aux routing) for MI355X -- flashinfer-bench solution entry.
 
 Shipped as ``main.py`` of a solution directory written by ``justgoal_amd.solution``; the entry
-point is ``main.py::run``, value-returning (destination_passing_style false), with the argument
-list of the definition (goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:286-288).
+point is ``main.py::run`` with the argument list of the definition
+(goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:286-288). It returns the output
+(destination_passing_style false), or, given an eleventh ``output`` argument, writes into it
+(the destination-passing form, kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t901/main.py:45-57).
 
 The HIP sources shipped beside this file are compiled with hipcc for gfx950 on first use (or a
 prebuilt ``libjustgoal_moe.so`` shipped beside it is loaded) and bound through ctypes, as the
@@ -85,11 +87,18 @@ def _scalar(x, cast):
 @torch.no_grad()
 def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
         gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-        routed_scaling_factor):
-    """bf16 [T, 7168] output of the DS-V3 FP8 block-scale MoE layer."""
+        routed_scaling_factor, output=None):
+    """bf16 [T, 7168] output of the DS-V3 FP8 block-scale MoE layer (written into ``output``
+    when it is given, then returned)."""
     T = int(routing_logits.shape[0])
     dev = hidden_states.device
-    out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=dev)
+    if output is None:
+        out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=dev)
+    elif (output.dtype != torch.bfloat16 or tuple(output.shape) != (T, HIDDEN)
+          or not output.is_contiguous() or output.device != dev):
+        raise ValueError("output must be a contiguous bf16 [T, 7168] tensor on the inputs' device")
+    else:
+        out = output
     if T == 0:
         return out
     logits = routing_logits.contiguous().to(torch.float32)

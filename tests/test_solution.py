@@ -41,6 +41,14 @@ def test_schema_and_sources(tmp_path):
         assert src in names
 
 
+def test_dps_flag(tmp_path):
+    d = json.load(open(solution.write_solution(str(tmp_path), dps=True)))
+    assert d["spec"]["destination_passing_style"] is True
+    import inspect
+    params = list(inspect.signature(load_main(str(tmp_path)).run).parameters)
+    assert len(params) == 11 and params[-1] == "output"
+
+
 def test_shipped_sources_compile(tmp_path):
     """The entry point's own build recipe, on the shipped files only (hipcc cross-compiles)."""
     solution.write_solution(str(tmp_path))
@@ -66,5 +74,10 @@ def test_entry_point_matches_library(gpu, tmp_path):
     args = [a.to(gpu) for a in args]
     got = m.run(*args, torch.tensor(0), torch.tensor(2.5))
     ref = run(*args, 0, 2.5)
+    dst = torch.full_like(ref, float("nan"))
+    assert m.run(*args, 0, 2.5, dst) is dst  # destination-passing form
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+    assert torch.equal(dst, ref)
+    with pytest.raises(ValueError):
+        m.run(*args, 0, 2.5, torch.empty(ref.shape, dtype=torch.float32, device=gpu))
