@@ -31,7 +31,7 @@ extern "C" {
 #endif
 
 #define MOE_OK 0
-#define MOE_ERR_INVALID_ARG (-1)     /* null pointer, negative T, bad scalar */
+#define MOE_ERR_INVALID_ARG (-1)     /* null pointer, negative T, T above the limit, bad scalar */
 #define MOE_ERR_GEOMETRY (-2)        /* geometry the kernels do not support */
 #define MOE_ERR_NO_DEVICE (-3)       /* device query failed or the device is not gfx950 */
 
@@ -40,8 +40,8 @@ extern "C" {
 
 /* Operator geometry. The DeepSeek-V3 values are {7168, 2048, 256, 32, 8, 8, 4, MOE_ROUTING_DS}. */
 typedef struct moe_geometry {
-  int hidden;          /* H, multiple of 128 */
-  int intermediate;    /* I, multiple of 128 */
+  int hidden;          /* H, multiple of 128, at most 16384 */
+  int intermediate;    /* I, multiple of 128, at most 16384 */
   int num_experts;     /* E, multiple of 64, <= 512 */
   int local_experts;   /* E_l, 1..min(E, 256) */
   int top_k;           /* 1..8 */
@@ -59,6 +59,8 @@ typedef struct moe_geometry {
  * Same argument order and meaning. Difference: the workspace need not be zeroed on entry (the
  * reference requires a zeroed one, t1/main.py:77-83; no kernel here keeps state in it), and it
  * is sized by moe_workspace_bytes(T). Calls that overlap in time need distinct workspaces.
+ * T is limited by 32-bit buffer offsets: T*hidden < 2^31 - 16 and T*min(top_k, E_local)*
+ * intermediate*2 < 2^31 (DS-V3: T <= 65535); larger T returns MOE_ERR_INVALID_ARG.
  */
 int moe_run(const void* logits, const void* bias, const void* hs, const void* hs_scale,
             const void* w13, const void* s13, const void* w2, const void* s2, int local_offset,

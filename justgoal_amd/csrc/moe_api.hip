@@ -25,7 +25,7 @@ bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 int check_geometry(const moe_geometry* g) {
   if (!g) return MOE_ERR_INVALID_ARG;
   if (g->hidden <= 0 || g->hidden % 128 || g->hidden > 16384 || g->intermediate <= 0 ||
-      g->intermediate % 128)
+      g->intermediate % 128 || g->intermediate > 16384)
     return MOE_ERR_GEOMETRY;
   const int E = g->num_experts;
   if (E <= 0 || E % 64 || E > 512 || !is_pow2(E / 64)) return MOE_ERR_GEOMETRY;
@@ -47,6 +47,16 @@ int check_geometry(const moe_geometry* g) {
 int64_t max_pairs(const moe_geometry* g, int T) {
   const int k = g->top_k < g->local_experts ? g->top_k : g->local_experts;
   return (int64_t)T * k;
+}
+
+// Most tokens one moe_run call takes. The kernels address activations, C rows and their scales
+// with 32-bit buffer offsets: T*H must stay below the large-tile kernels' out-of-range marker
+// (2^31 - 16) and max_pairs*I*2 (bytes of C) below 2^31. DS-V3: 65535 tokens.
+int64_t token_limit(const moe_geometry* g) {
+  const int64_t k = g->top_k < g->local_experts ? g->top_k : g->local_experts;
+  const int64_t by_a = (int64_t)(0x7ffffff0 - 1) / g->hidden;
+  const int64_t by_c = (int64_t)0x7fffffff / (k * g->intermediate * 2);
+  return by_a < by_c ? by_a : by_c;
 }
 
 void layout(const moe_geometry* g, int T, int64_t* off) {
@@ -200,7 +210,7 @@ int moe_run_ex(const moe_geometry* geom, const void* logits, const void* bias, c
                void* stream_) {
   int rc = check_geometry(geom);
   if (rc != MOE_OK) return rc;
-  if (T < 0) return MOE_ERR_INVALID_ARG;
+  if (T < 0 || T > token_limit(geom)) return MOE_ERR_INVALID_ARG;
   if (T == 0) return MOE_OK;
   if (!logits || !hs || !hs_scale || !w13 || !s13 || !w2 || !s2 || !out || !workspace)
     return MOE_ERR_INVALID_ARG;
@@ -245,7 +255,9 @@ int moe_quantize_activations(const void* x, int T, int H, void* q, void* scale, 
 const char* moe_error_string(int rc) {
   switch (rc) {
     case MOE_OK: return "success";
-    case MOE_ERR_INVALID_ARG: return "invalid argument (null pointer or negative token count)";
+    case MOE_ERR_INVALID_ARG:
+      return "invalid argument (null pointer, negative token count, or more tokens than one call "
+             "takes)";
     case MOE_ERR_GEOMETRY: return "unsupported MoE geometry";
     case MOE_ERR_NO_DEVICE: return "no gfx950 (MI355X) device is current";
     default: return rc > 0 ? hipGetErrorString((hipError_t)rc) : "unknown error";

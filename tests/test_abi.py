@@ -56,6 +56,7 @@ def test_layout_regions_ordered_and_aligned():
     Geometry(7168, 2048, 256, 32, 8, 3, 2, ROUTING_DS),    # groups do not divide E
     Geometry(7168, 2048, 256, 32, 8, 8, 9, ROUTING_DS),    # topk_group > n_group
     Geometry(7168, 2048, 256, 32, 8, 8, 4, 7),             # unknown routing method
+    Geometry(7168, 16512, 256, 32, 8, 8, 4, ROUTING_DS),   # I above 16384
 ])
 def test_bad_geometry_rejected(bad):
     L = _lib.lib()
@@ -73,6 +74,19 @@ def test_null_pointers_and_negative_T_rejected_on_host():
     assert L.moe_run(None, *args[1:], 0, 2.5, 1, 1, 16, None) == -1
     assert L.moe_run(*args, 0, 2.5, None, 1, 16, None) == -1
     assert L.moe_run(*args, 0, 2.5, 1, None, 16, None) == -1
+
+
+def test_token_limit_rejected_on_host():
+    # C rows are addressed with 32-bit offsets: T * 8 * 2048 * 2 bytes must stay below 2^31
+    L = _lib.lib()
+    args = [1] * 8
+    assert L.moe_run(*args, 0, 2.5, 1, 1, 65536, None) == -1
+    assert "tokens" in L.moe_error_string(-1).decode()
+    # at the limit the host checks pass and the call reaches the device query (none here)
+    assert L.moe_run(*args, 0, 2.5, 1, 1, 65535, None) != -1
+    g = QWEN3.c_struct()  # 8 * 1536 * 2 bytes of C per token: 87381 tokens
+    assert L.moe_run_ex(ctypes.byref(g), *args, 0, 1.0, 1, 1, 87382, None) == -1
+    assert L.moe_run_ex(ctypes.byref(g), *args, 0, 1.0, 1, 1, 87381, None) != -1
 
 
 def test_zero_tokens_is_a_no_op():
