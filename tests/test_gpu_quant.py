@@ -1,6 +1,7 @@
 """GPU parity of the activation-quantisation kernel (moe_quantize_activations) against the CPU
 oracle: e4m3 codes and fp32 scales bit-exact. Cases: random rows with edge blocks (all-zero,
-values in the e4m3 subnormal range, exact rounding ties, a huge dynamic range), ragged shapes
+values in the e4m3 subnormal range, exact rounding ties, a huge dynamic range), every finite
+bf16 value under each of 48 block maxima (subnormal to largest finite), ragged shapes
 (T not a multiple of 16, H not a multiple of 512), the full DS-V3 T=4096 batch, and the chain
 quantise -> operator against the oracle on the same bf16 input.
 """
@@ -62,6 +63,40 @@ def test_random_and_edges(gpu):
     x = torch.randn(300, 7168, generator=torch.Generator().manual_seed(1)).bfloat16()
     x[:8] = edge_rows(7168)
     check(x, gpu)
+
+
+def every_value_blocks(amaxes, H=7168):
+    """Blocks of 128 whose first element is amax and the rest run through every finite bf16 value
+    with |x| <= amax (zero padding), so each block's divisor is amax / 448 and every quotient the
+    kernel can meet under that divisor occurs once."""
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    allv = (bits << 16).view(np.float32)
+    allv = allv[np.isfinite(allv)]
+    blocks = []
+    for a in amaxes:
+        vals = allv[np.abs(allv) <= a]
+        n = -(-vals.size // 127)
+        body = np.zeros(n * 127, np.float32)
+        body[:vals.size] = vals
+        blk = np.concatenate([np.full((n, 1), a, np.float32), body.reshape(n, 127)], axis=1)
+        blocks.append(blk)
+    b = np.concatenate(blocks)
+    per_row = H // 128
+    rows = -(-b.shape[0] // per_row)
+    out = np.zeros((rows * per_row, 128), np.float32)
+    out[:b.shape[0]] = b
+    return torch.from_numpy(out.reshape(rows, H)).bfloat16()
+
+
+def test_every_bf16_value_under_each_amax(gpu):
+    """The kernel divides with a reciprocal and one remainder correction (tiny blocks rescaled);
+    every quotient reachable under these 48 divisors must give the correctly rounded division's
+    code, signed zeros included."""
+    g = np.random.default_rng(5)
+    special = [0x0001, 0x0002, 0x007f, 0x0080, 0x0081, 0x3f80, 0x43e0, 0x7f7f, 0x7f00, 0x0100]
+    rnd = [int(b) for b in g.integers(0x0001, 0x7f7f, 38)]
+    amaxes = [float(np.array([b << 16], np.uint32).view(np.float32)[0]) for b in special + rnd]
+    check(every_value_blocks(amaxes), gpu)
 
 
 @pytest.mark.parametrize("T,H", [(1, 128), (17, 384), (33, 640), (5, 4096)])
