@@ -692,15 +692,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
 }  // namespace
 
 static int big_grid(long long max_items) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    cus = (hipGetDevice(&dev) == hipSuccess &&
-           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-           n > 0)
-              ? n
-              : 256;
-  }
+  const int cus = device_cu_count();
   long long g = cus;  // the LDS rings leave room for one workgroup per CU
   if (g > max_items) g = max_items;
   return g < 1 ? 1 : (int)g;

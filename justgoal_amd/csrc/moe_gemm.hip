@@ -19,6 +19,8 @@
 // [32g, 32g+32) of its row for both operands. For the bf16 MFMA (K=32 per instruction) chunk c
 // of those 32 values is fed to instruction c, so instruction c covers K = {32g + 8c .. +8 : g}.
 // Because A and B use the same map, each output still sums over every K exactly once.
+#include <mutex>
+
 #include "moe_device.h"
 #include "moe_kernels.h"
 
@@ -129,6 +131,22 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
   if (e != hipErrorNotSupported) return e;
   return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs,
                              4, stream);
+}
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::once_flag flags[kMaxDevices];
+  static int cus[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::call_once(flags[dev], [dev] {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                       n > 0
+                   ? n
+                   : 256;
+  });
+  return cus[dev];
 }
 
 hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,

@@ -69,6 +69,10 @@ hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* 
                              int max_pairs, int mt, hipStream_t stream);
 
 // out[t, :] = bf16(sum of partial rows of t's local pairs, ascending local expert), 0 if none.
+// Compute units of the current device, queried once per device (thread-safe); 256 when the
+// query fails. Sizes the persistent grids.
+int device_cu_count();
+
 hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,
                           uint16_t* out, hipStream_t stream);
 

@@ -488,15 +488,7 @@ __global__ __launch_bounds__(256) void gemm2_tile_kernel(
 }  // namespace
 
 static int tile_grid(int per_cu, long long max_items) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    cus = (hipGetDevice(&dev) == hipSuccess &&
-           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-           n > 0)
-              ? n
-              : 256;
-  }
+  const int cus = device_cu_count();
   long long g = (long long)cus * per_cu;
   if (g > max_items) g = max_items;
   return g < 1 ? 1 : (int)g;

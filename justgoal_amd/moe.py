@@ -12,7 +12,7 @@ scalars may be 0-d tensors, logits/bias/scales are coerced to fp32/bf16 contiguo
 must already be e4m3fn and contiguous. A ``None`` bias means zeros
 (kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t14107/main.py:97-98). The work runs in
 HIP kernels through the C ABI on the current torch stream; this module only checks arguments and
-owns the cached workspace.
+owns the cached workspaces (one per stream).
 """
 from __future__ import annotations
 
@@ -27,16 +27,27 @@ F8 = torch.float8_e4m3fn
 _WS: dict = {}
 
 
-def workspace(geom: Geometry, T: int, device) -> torch.Tensor:
-    """Cached uint8 workspace for (geometry, T, device); its contents need no initialisation."""
+def workspace(geom: Geometry, T: int, device, stream=None) -> torch.Tensor:
+    """The workspace ``run`` and ``route`` use on (device, stream): one buffer per stream that
+    grows to the largest ``moe_workspace_bytes`` seen (any buffer at least that large serves a
+    call with T tokens; its contents need no initialisation). Calls on one stream are ordered,
+    so they can share it; calls on different streams get different buffers, as calls that
+    overlap in time must. ``stream`` defaults to the device's current torch stream."""
     dev = torch.device(device)
-    key = (geom, int(T), dev)
+    if stream is None:
+        stream = torch.cuda.current_stream(dev)
+    key = (dev, int(stream.cuda_stream))
+    n = max(_lib.workspace_layout(geom, T)["total"], 1)
     ws = _WS.get(key)
-    if ws is None:
-        n = _lib.workspace_layout(geom, T)["total"]
-        ws = torch.empty(max(n, 1), dtype=torch.uint8, device=dev)
+    if ws is None or ws.numel() < n:
+        ws = torch.empty(n, dtype=torch.uint8, device=dev)
         _WS[key] = ws
     return ws
+
+
+def release_workspaces() -> None:
+    """Drops the cached per-stream workspaces (their memory returns to torch's allocator)."""
+    _WS.clear()
 
 
 def _scalar(x, cast):
@@ -156,8 +167,11 @@ def bind(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1
     if output is None:
         output = torch.empty((T, geom.hidden), dtype=torch.bfloat16, device=dev)
     tensors = (routing_logits, hidden_states, hss, gemm1_weights, s13, gemm2_weights, s2)
+    # a bound call owns its workspace, so bound calls on different streams never share one
+    ws = torch.empty(max(_lib.workspace_layout(geom, T)["total"], 1), dtype=torch.uint8,
+                     device=dev)
     return BoundCall(geom, tensors, routing_bias, _scalar(local_expert_offset, int),
-                     _scalar(routed_scaling_factor, float), output, workspace(geom, T, dev), T)
+                     _scalar(routed_scaling_factor, float), output, ws, T)
 
 
 @torch.no_grad()

@@ -119,16 +119,19 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
         if tuple(t.shape) != shape:
             raise ValueError(f"expected shape {shape}, got {tuple(t.shape)}")
     L = _lib()
-    key = (T, dev)
+    # one workspace per stream, grown to the largest call (calls on one stream are ordered;
+    # calls that may overlap, on different streams, get different buffers)
+    stream = torch.cuda.current_stream(dev)
+    key = (dev, int(stream.cuda_stream))
+    need = max(int(L.moe_workspace_bytes(T)), 1)
     ws = _WS.get(key)
-    if ws is None:
-        ws = _WS[key] = torch.empty(max(int(L.moe_workspace_bytes(T)), 1), dtype=torch.uint8,
-                                    device=dev)
+    if ws is None or ws.numel() < need:
+        ws = _WS[key] = torch.empty(need, dtype=torch.uint8, device=dev)
     rc = L.moe_run(logits.data_ptr(), None if bias is None else bias.data_ptr(),
                    hidden_states.data_ptr(), hss.data_ptr(), gemm1_weights.data_ptr(),
                    s13.data_ptr(), gemm2_weights.data_ptr(), s2.data_ptr(),
                    _scalar(local_expert_offset, int), _scalar(routed_scaling_factor, float),
-                   out.data_ptr(), ws.data_ptr(), T, torch.cuda.current_stream(dev).cuda_stream)
+                   out.data_ptr(), ws.data_ptr(), T, stream.cuda_stream)
     if rc != 0:
         raise RuntimeError(f"moe_run failed ({rc}): {L.moe_error_string(rc).decode()}")
     return out

@@ -15,7 +15,7 @@ import torch
 import oracle
 from justgoal_amd import inputs as jin
 from justgoal_amd.geometry import DS_V3, QWEN3, ROUTING_DS, ROUTING_SOFTMAX, Geometry
-from justgoal_amd.moe import run, workspace, workspace_views
+from justgoal_amd.moe import release_workspaces, run, workspace, workspace_views
 
 pytestmark = pytest.mark.gpu
 
@@ -200,6 +200,39 @@ def test_dps_output(gpu):
     res = run(**kw, output=dst, geometry=MINI_DS)
     assert res.data_ptr() == dst.data_ptr()
     assert torch.equal(dst, ref)
+
+
+def test_workspace_per_stream_grows_and_is_not_shared(gpu):
+    """run() keeps one workspace per stream that grows to the largest call: a call after a
+    larger one runs in the larger buffer and must match a call in a buffer of its own size; two
+    streams running at once use different buffers, so both results stay exact."""
+    w = weights_for(MINI_DS, gpu)[1]
+
+    def kw(T, seed):
+        act = to_dev(jin.make_activations(MINI_DS, T, seed=seed), gpu)
+        return dict(act, gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2],
+                    gemm2_weights_scale=w[3], local_expert_offset=0, routed_scaling_factor=2.5,
+                    geometry=MINI_DS)
+
+    cases = [(40, 5), (300, 6), (17, 7)]
+    args = {c: kw(*c) for c in cases}
+    release_workspaces()
+    grown = {c: run(**args[c]).clone() for c in cases}  # 17 runs in the 300-token buffer
+    torch.cuda.synchronize()
+    for c in cases:
+        release_workspaces()
+        assert torch.equal(run(**args[c]), grown[c]), c
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        a = run(**args[(300, 6)])
+    with torch.cuda.stream(s2):
+        b = run(**args[(40, 5)])
+    torch.cuda.synchronize()
+    assert torch.equal(a, grown[(300, 6)]) and torch.equal(b, grown[(40, 5)])
+    assert (workspace(MINI_DS, 300, gpu, s1).data_ptr()
+            != workspace(MINI_DS, 40, gpu, s2).data_ptr())
+    release_workspaces()
 
 
 # Routing workgroups hold 4 tokens up to T=256 and 16 above: both sides of the switch and ragged
