@@ -29,7 +29,7 @@ sys.path.insert(0, HERE)
 from justgoal_amd import _lib  # noqa: E402
 from justgoal_amd import inputs as jin  # noqa: E402
 from justgoal_amd.geometry import BLOCK, bytes_per_token, flops_per_pair, weight_bytes_per_expert  # noqa: E402
-from justgoal_amd.moe import bind, workspace, workspace_views  # noqa: E402
+from justgoal_amd.moe import bind, workspace_views  # noqa: E402
 
 METRIC = "ms/call + TFLOPS, DS-V3 FP8 MoE at T=64 and T=4096; % of FP8 MFMA/HBM peak"
 PEAK_HBM_GBS = 8000.0
@@ -42,8 +42,10 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def routing_stats(geom, T, dev):
-    v = workspace_views(geom, T, workspace(geom, T, dev))
+def routing_stats(geom, T, ws):
+    """Routed pairs, active local experts and tokens with a local pair, read from the workspace
+    of the call that just ran."""
+    v = workspace_views(geom, T, ws)
     counts = v["counts"].cpu()
     pairs = int(counts.sum())
     active = int((counts > 0).sum())
@@ -115,7 +117,7 @@ def measure(cfg, weights_dev, steps, warmup, dev, seed=None):
     call = bind(**kw, geometry=geom)
     ms = time_calls(call, steps, warmup, dev)
     st = stage_times(call, max(5, min(steps, 20)), dev)
-    pairs, active, tok_local = routing_stats(geom, cfg.tokens, dev)
+    pairs, active, tok_local = routing_stats(geom, cfg.tokens, call.workspace)
     flops, bytes_, g1_flops, g1_bytes = algorithmic(geom, cfg.tokens, pairs, active, tok_local)
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = bytes_ / (ms * 1e-3) / 1e9

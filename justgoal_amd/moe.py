@@ -130,6 +130,7 @@ class BoundCall:
 
     def __init__(self, geom, tensors, bias, off, rsf, output, ws, T):
         self.geom, self.T, self.output = geom, T, output
+        self.workspace = ws  # this call's own workspace (routing results stay readable here)
         self._keep = (tensors, bias, output, ws)
         self._g = geom.c_struct()
         self._fn = _lib.lib().moe_run_ex

@@ -15,7 +15,7 @@ import torch
 import oracle
 from justgoal_amd import inputs as jin
 from justgoal_amd.geometry import DS_V3, QWEN3, ROUTING_DS, ROUTING_SOFTMAX, Geometry
-from justgoal_amd.moe import release_workspaces, run, workspace, workspace_views
+from justgoal_amd.moe import bind, release_workspaces, run, workspace, workspace_views
 
 pytestmark = pytest.mark.gpu
 
@@ -200,6 +200,24 @@ def test_dps_output(gpu):
     res = run(**kw, output=dst, geometry=MINI_DS)
     assert res.data_ptr() == dst.data_ptr()
     assert torch.equal(dst, ref)
+
+
+def test_bound_call_matches_run(gpu):
+    """bind() validates once; the bound call gives run()'s output bit for bit and keeps the
+    routing results in its own workspace (the benchmark reads pair counts from there)."""
+    w = weights_for(MINI_DS, gpu)[1]
+    act = to_dev(jin.make_activations(MINI_DS, 77, seed=8), gpu)
+    kw = dict(act, gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2],
+              gemm2_weights_scale=w[3], local_expert_offset=0, routed_scaling_factor=2.5,
+              geometry=MINI_DS)
+    ref = run(**kw).clone()
+    ref_counts = workspace_views(MINI_DS, 77, workspace(MINI_DS, 77, gpu))["counts"].clone()
+    call = bind(**kw)
+    out = call()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    counts = workspace_views(MINI_DS, 77, call.workspace)["counts"]
+    assert torch.equal(counts, ref_counts) and int(counts.sum()) > 0
 
 
 def test_workspace_per_stream_grows_and_is_not_shared(gpu):
