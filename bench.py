@@ -118,6 +118,8 @@ def measure(cfg, weights_dev, steps, warmup, dev, seed=None):
     ms = time_calls(call, steps, warmup, dev)
     st = stage_times(call, max(5, min(steps, 20)), dev)
     pairs, active, tok_local = routing_stats(geom, cfg.tokens, call.workspace)
+    if pairs == 0:
+        raise RuntimeError(f"{cfg.name}: no routed pairs read back from the call's workspace")
     flops, bytes_, g1_flops, g1_bytes = algorithmic(geom, cfg.tokens, pairs, active, tok_local)
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = bytes_ / (ms * 1e-3) / 1e9

@@ -1,0 +1,51 @@
+"""bench.py on the host: the one-GPU guard, the unit figures its roofline arithmetic rests on, and
+the routing statistics it reads back from a call's workspace (no GPU needed)."""
+import os
+import subprocess
+import sys
+
+import torch
+
+from justgoal_amd import _lib
+from justgoal_amd.geometry import DS_V3, QWEN3, bytes_per_token, flops_per_pair, weight_bytes_per_expert
+from justgoal_amd.moe import workspace_views
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_unit_figures():
+    # DS-V3: 6*H*I FLOPs per local pair; W13 + W2 fp8 with their fp32 128x128 block scales per
+    # active expert; fp8 row + scales + fp32 logits + bf16 output row per token
+    assert flops_per_pair(DS_V3) == 88_080_384
+    assert weight_bytes_per_expert(DS_V3) == 3 * 2048 * 7168 + 4 * (32 * 56 + 56 * 16)
+    assert weight_bytes_per_expert(DS_V3) == 44_050_944
+    assert bytes_per_token(DS_V3) == 22_752
+    assert flops_per_pair(QWEN3) == 37_748_736
+    flops, nbytes, g1_flops, g1_bytes = bench.algorithmic(DS_V3, 64, 55, 16, 40)
+    assert flops == 55 * 88_080_384 and g1_flops == 55 * 2 * 7168 * 4096
+    assert nbytes == 16 * 44_050_944 + 64 * 22_752 + 2 * 256
+    # GEMM1 + SwiGLU: W13 + S13 of 16 experts, 40 routed token rows with scales, 55 bf16 C rows
+    assert g1_bytes == 16 * (4096 * 7168 + 4 * 32 * 56) + 40 * (7168 + 4 * 56) + 55 * 2048 * 2
+
+
+def test_routing_stats_read_the_given_workspace():
+    T = 8
+    ws = torch.zeros(_lib.workspace_layout(DS_V3, T)["total"], dtype=torch.uint8)
+    v = workspace_views(DS_V3, T, ws)
+    v["counts"][:] = 0
+    v["counts"][3] = 2
+    v["counts"][30] = 1
+    v["pair_of"][:] = -1
+    v["pair_of"][0, 1] = 0
+    v["pair_of"][5, 0] = 1
+    v["pair_of"][5, 7] = 2
+    assert bench.routing_stats(DS_V3, T, ws) == (3, 2, 2)
