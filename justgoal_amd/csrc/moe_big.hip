@@ -428,7 +428,7 @@ struct B2Scalars {
 };
 
 // MS/NS: 16-row/16-column sub-tiles per compute wave; WM x WN compute waves (wave index w:
-// wm = w % WM, wn = w / WM), so BM = 16*MS*WM and BN = 16*NS*WN; wave WM*WN is the producer.
+// wm = w / WN, wn = w % WN), so BM = 16*MS*WM and BN = 16*NS*WN; wave WM*WN is the producer.
 template <int MS, int NS, int D, int WM, int WN>
 __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
@@ -532,7 +532,10 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     return;
   }
 
-  const int wm = w % WM, wn = w / WM;
+  // Row-major wave order (w = wm*WN + wn): the two compute waves that share a SIMD (w and w+4)
+  // hold row slices wm and wm+2, so the all-padding slices of a part-filled tile (which skip
+  // their MFMAs below) spread over the SIMDs instead of idling some while others carry two.
+  const int wm = w / WN, wn = w % WN;
   const int r16 = lane & 15, g = lane >> 4;
   const __amdgpu_buffer_rsrc_t wgtres = make_rsrc(sorted_w, (uint32_t)max_pairs * 4);
   const __amdgpu_buffer_rsrc_t s2res = make_rsrc(s2, (uint32_t)E_l * (H / kBlock) * NKB * 4);
@@ -610,68 +613,97 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = v4f{0.f, 0.f, 0.f, 0.f};
-    int kb = 0;
-    do {
-      const int d = slot, dn = slot + 1 == D ? 0 : slot + 1;
-      const uint32_t ab = lds_addr(&aring[d][0]);
-      const float sw = cur.sc.get(kb);
-      lds_wait_all();  // the head fragments have landed
-      v8bf bw[NS][4];
+    // A wave whose 16*MS rows of the tile are all padding only keeps the workgroup's per-step
+    // barriers and reads the next item's head at its last step.
+    const bool busy = cur.s.m0 + wm * MS * 16 < cur.s.cnt;
+    // The head fragments come from asm LDS reads that the compiler takes as complete at once;
+    // where the two loop forms join it may copy them, so both forms wait for them first.
+    auto fence_head = [&] {
+      lds_wait_all();
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns) {
         lds_fence(wq[ns][0]);
         lds_fence(wq[ns][1]);
-        const uint32_t wv[8] = {wq[ns][0][0], wq[ns][0][1], wq[ns][0][2], wq[ns][0][3],
-                                wq[ns][1][0], wq[ns][1][1], wq[ns][1][2], wq[ns][1][3]};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          v2bf p0, p1, p2, p3;
-          fp8x4_to_bf16x4((int)wv[2 * c], p0, p1);
-          fp8x4_to_bf16x4((int)wv[2 * c + 1], p2, p3);
-          bw[ns][c] = v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-        }
       }
 #pragma unroll
       for (int c = 0; c < 4; ++c) lds_fence(a[0][c]);
-      // Column sub-tiles [n0, n1) of row sub-tile ms, their four K-chunk MFMAs interleaved
-      // (chunk outer) so that consecutive MFMAs are independent (chained per sub-tile they
-      // measured 2% slower), then the s2 block scale.
-      auto mma_row = [&](int ms, int n0, int n1, const v4u(&x)[4]) {
-        v4f t[NS];
+    };
+    if (!busy) {
+      int kb = 0;
+      do {
+        const int dn = slot + 1 == D ? 0 : slot + 1;
+        lds_wait_all();
+        __builtin_amdgcn_s_barrier();
+        if (kb + 1 == NKB) read_head(dn);
+        slot = dn;
+        ++kb;
+      } while (kb < NKB);
+      fence_head();
+    } else {
+      int kb = 0;
+      do {
+        const int d = slot, dn = slot + 1 == D ? 0 : slot + 1;
+        const uint32_t ab = lds_addr(&aring[d][0]);
+        const float sw = cur.sc.get(kb);
+        lds_wait_all();  // the head fragments have landed
+        v8bf bw[NS][4];
 #pragma unroll
-        for (int ns = 0; ns < NS; ++ns) t[ns] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int ns = 0; ns < NS; ++ns) {
+          lds_fence(wq[ns][0]);
+          lds_fence(wq[ns][1]);
+          const uint32_t wv[8] = {wq[ns][0][0], wq[ns][0][1], wq[ns][0][2], wq[ns][0][3],
+                                  wq[ns][1][0], wq[ns][1][1], wq[ns][1][2], wq[ns][1][3]};
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+          for (int c = 0; c < 4; ++c) {
+            v2bf p0, p1, p2, p3;
+            fp8x4_to_bf16x4((int)wv[2 * c], p0, p1);
+            fp8x4_to_bf16x4((int)wv[2 * c + 1], p2, p3);
+            bw[ns][c] = v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) lds_fence(a[0][c]);
+        // Column sub-tiles [n0, n1) of row sub-tile ms, their four K-chunk MFMAs interleaved
+        // (chunk outer) so that consecutive MFMAs are independent (chained per sub-tile they
+        // measured 2% slower), then the s2 block scale.
+        auto mma_row = [&](int ms, int n0, int n1, const v4u(&x)[4]) {
+          v4f t[NS];
+#pragma unroll
+          for (int ns = 0; ns < NS; ++ns) t[ns] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int ns = n0; ns < n1; ++ns)
+              t[ns] = mfma_bf16_16x16x32(bw[ns][c], __builtin_bit_cast(v8bf, x[c]), t[ns]);
 #pragma unroll
           for (int ns = n0; ns < n1; ++ns)
-            t[ns] = mfma_bf16_16x16x32(bw[ns][c], __builtin_bit_cast(v8bf, x[c]), t[ns]);
 #pragma unroll
-        for (int ns = n0; ns < n1; ++ns)
+            for (int i = 0; i < 4; ++i) acc[ms][ns][i] = fmaf(t[ns][i], sw, acc[ms][ns][i]);
+        };
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[ms][ns][i] = fmaf(t[ns][i], sw, acc[ms][ns][i]);
-      };
+        for (int ms = 0; ms < MS; ++ms) {
+          v4u(&x)[4] = a[ms & 1];
+          if (ms + 1 < MS) {
+            read_a(ab, ms + 1, a[(ms + 1) & 1]);
+            mma_row(ms, 0, NS, x);
+            lds_wait_all();
 #pragma unroll
-      for (int ms = 0; ms < MS; ++ms) {
-        v4u(&x)[4] = a[ms & 1];
-        if (ms + 1 < MS) {
-          read_a(ab, ms + 1, a[(ms + 1) & 1]);
-          mma_row(ms, 0, NS, x);
-          lds_wait_all();
-#pragma unroll
-          for (int c = 0; c < 4; ++c) lds_fence(a[(ms + 1) & 1][c]);
-        } else {
-          // last row sub-tile (a[1]; a[0] and wq are free for the next block's head)
-          mma_row(ms, 0, NS / 2, x);
-          // Block kb+1 has landed and slot d is no longer read. After the last block this
-          // barrier pairs with the producer's final one and the head read is unused.
-          __builtin_amdgcn_s_barrier();
-          read_head(dn);  // (pinning these ahead of the MFMAs, as in GEMM1, measured slower here)
-          mma_row(ms, NS / 2, NS, x);
+            for (int c = 0; c < 4; ++c) lds_fence(a[(ms + 1) & 1][c]);
+          } else {
+            // last row sub-tile (a[1]; a[0] and wq are free for the next block's head)
+            mma_row(ms, 0, NS / 2, x);
+            // Block kb+1 has landed and slot d is no longer read. After the last block this
+            // barrier pairs with the producer's final one and the head read is unused.
+            __builtin_amdgcn_s_barrier();
+            read_head(dn);  // (pinning these ahead of the MFMAs, as in GEMM1, measured slower here)
+            mma_row(ms, NS / 2, NS, x);
+          }
         }
-      }
-      slot = dn;
-      ++kb;
-    } while (kb < NKB);
+        slot = dn;
+        ++kb;
+      } while (kb < NKB);
+      fence_head();
+    }
     vm_wait<0>();
     finish(nn);
 
