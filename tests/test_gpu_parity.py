@@ -58,12 +58,14 @@ def subset_tokens(inp_cpu, tok):
 
 
 def check_case(geom, T, device, seed=0, tokens_checked=None, local_offset=0, bias=True,
-               skew=(0, 0.0), rsf=None):
+               skew=(0, 0.0), rsf=None, logits=None):
     (w_cpu, w_dev) = weights_for(geom, device)
     act = jin.make_activations(geom, T, seed=seed, skew_experts=skew[0], skew_offset=skew[1],
                                local_offset=local_offset)
     if not bias:
         act["routing_bias"] = None
+    if logits is not None:
+        act["routing_logits"] = logits
     inp_cpu = dict(act, gemm1_weights=w_cpu[0], gemm1_weights_scale=w_cpu[1],
                    gemm2_weights=w_cpu[2], gemm2_weights_scale=w_cpu[3],
                    local_expert_offset=local_offset,
@@ -218,6 +220,50 @@ def test_bound_call_matches_run(gpu):
     assert torch.equal(out, ref)
     counts = workspace_views(MINI_DS, 77, call.workspace)["counts"]
     assert torch.equal(counts, ref_counts) and int(counts.sum()) > 0
+
+
+SEG_GEOM = Geometry(256, 256, 64, 64, 8, 1, 1, ROUTING_SOFTMAX, "segments")
+
+
+def logits_for_counts(counts, T, E, top_k=8):
+    """Softmax-routing logits under which local expert e receives exactly counts[e] tokens:
+    the pair slots, sorted by expert, are dealt to tokens in turn, so every token gets top_k
+    distinct experts (each count <= T); the chosen experts get logits 4..5 (distinct per
+    token), the others -4."""
+    slots = [e for e, c in enumerate(counts) for _ in range(c)]
+    assert len(slots) == T * top_k and max(counts) <= T
+    lg = torch.full((T, E), -4.0)
+    for i, e in enumerate(slots):
+        t = i % T
+        lg[t, e] = 4.0 + (i // T) / top_k
+    return lg
+
+
+def boundary_counts(T, E=64, top_k=8):
+    """Per-expert pair counts at and around every 16-row multiple up to the largest tile (and
+    empty experts), padded with even counts to T*top_k pairs."""
+    want = [0, 1, 2, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64, 65, 95, 96, 97, 127, 128, 129,
+            159, 160, 161, 191, 192, 193, 255, 256, 257]
+    counts = []
+    for c in want:
+        if c <= T and len(counts) < E // 2 and sum(counts) + c <= 0.8 * T * top_k:
+            counts.append(c)
+    rest = T * top_k - sum(counts)
+    n = E - len(counts)
+    counts += [rest // n + (1 if i < rest % n else 0) for i in range(n)]
+    assert max(counts) <= T and sum(counts) == T * top_k
+    return counts
+
+
+@pytest.mark.parametrize("T", [128, 256, 512, 1024])
+def test_segment_length_boundaries(gpu, T):
+    """Expert segments of exactly 1, 15, 16, 17, 31, 32, 33, ... pairs (and empty experts): the
+    tile edges of the streaming (T=128), LDS-tile (T=256) and large-tile (T=512, 1024) kernels,
+    including large-tile waves whose rows of a tile are all padding."""
+    counts = boundary_counts(T)
+    lg = logits_for_counts(counts, T, SEG_GEOM.num_experts)
+    _, ws = check_case(SEG_GEOM, T, gpu, seed=9, logits=lg, bias=False, rsf=1.0)
+    assert ws["counts"].cpu().tolist() == counts
 
 
 def test_workspace_per_stream_grows_and_is_not_shared(gpu):
