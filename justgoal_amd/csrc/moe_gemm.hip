@@ -71,17 +71,24 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
   *(uint4*)(out + (size_t)t * H + c) = o;
 }
 
+// Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from a sweep
+// over T = 64..16384 (DS-V3) and 128..1024 (Qwen3-style): GEMM1 streams weights up to 4
+// expected rows, uses the LDS-tiled kernels up to 63 and the large tiles from 64; GEMM2 streams
+// up to 3 and uses the large tiles above (their padding-row skip keeps part-filled 128-row
+// tiles cheap; the LDS-tiled GEMM2 lost to them everywhere). The streaming kernels' 16-row
+// items re-stream an expert's weights once per 16 rows, so they only win while segments are
+// that short.
 #ifndef JG_STREAM_MAX_ROWS
-#define JG_STREAM_MAX_ROWS 16
+#define JG_STREAM_MAX_ROWS 4
 #endif
-
-// Expected pairs per expert from which the large-tile kernels take over.
 #ifndef JG_BIG_ROWS
 #define JG_BIG_ROWS 64
 #endif
-
-#ifndef JG_G2T_MT
-#define JG_G2T_MT 0
+#ifndef JG_G2_STREAM_MAX_ROWS
+#define JG_G2_STREAM_MAX_ROWS 3
+#endif
+#ifndef JG_G2_BIG_ROWS
+#define JG_G2_BIG_ROWS 4
 #endif
 
 #ifndef JG_TILE_MT8_ROWS
@@ -117,18 +124,14 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
                         float* partial, int H, int I, int E_l, int max_pairs, int rows_hint,
                         hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= JG_STREAM_MAX_ROWS)
+  if (rows_hint <= JG_G2_STREAM_MAX_ROWS)
     return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
                                max_pairs, stream_mt(rows_hint), stream);
-  if (rows_hint >= JG_BIG_ROWS) {
+  if (rows_hint >= JG_G2_BIG_ROWS) {
     const hipError_t b = launch_gemm2_big(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
                                           max_pairs, stream);
     if (b != hipErrorNotSupported) return b;
   }
-  const hipError_t e = launch_gemm2_tile(C, w2, s2, counts, offsets, sorted_w, partial, H, I,
-                                         E_l, max_pairs, JG_G2T_MT ? JG_G2T_MT : tile_mt(rows_hint),
-                                         stream);
-  if (e != hipErrorNotSupported) return e;
   return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs,
                              4, stream);
 }

@@ -63,11 +63,6 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
                              const float* s13, const int32_t* counts, const int32_t* offsets,
                              const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                              int max_pairs, int mt, hipStream_t stream);
-hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* s2,
-                             const int32_t* counts, const int32_t* offsets,
-                             const float* sorted_w, float* partial, int H, int I, int E_l,
-                             int max_pairs, int mt, hipStream_t stream);
-
 // out[t, :] = bf16(sum of partial rows of t's local pairs, ascending local expert), 0 if none.
 // Compute units of the current device, queried once per device (thread-safe); 256 when the
 // query fails. Sizes the persistent grids.

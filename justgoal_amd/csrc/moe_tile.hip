@@ -1,14 +1,15 @@
-// LDS-tiled grouped GEMMs for segments of tens to thousands of pairs per expert.
+// LDS-tiled grouped GEMM1 + SwiGLU for segments of a few to tens of pairs per expert (GEMM2 of
+// that size runs on the large-tile kernels, whose padding-row skip measured faster).
 //
-// A workgroup (4 waves) computes a BM x 64 tile of one expert's GEMM1 output (BM = 16*MT pairs;
-// for GEMM2, BM x 64*NW). Everything reaches LDS by DMA (buffer_load ... lds), so the only
-// VGPRs spent on memory are the MFMA fragments of the current K block:
+// A workgroup (4 waves) computes a BM x 64 tile of one expert's GEMM1 output (BM = 16*MT pairs).
+// Everything reaches LDS by DMA (buffer_load ... lds), so the only VGPRs spent on memory are the
+// MFMA fragments of the current K block:
 //
-// * The activation tile (BM rows x one 128-wide K block: fp8 hidden-state rows for GEMM1, bf16 C
-//   rows for GEMM2) is gathered straight from the token rows into a ring of D LDS slots shared
-//   by the four waves, each wave issuing a quarter of the DMA instructions. GEMM1 also stages the
-//   rows' activation scales (4-byte DMA).
-// * Each wave streams the weight rows of its own 16*NW output columns into a private ring.
+// * The activation tile (BM fp8 hidden-state rows x one 128-wide K block) is gathered straight
+//   from the token rows into a ring of D LDS slots shared by the four waves, each wave issuing a
+//   quarter of the DMA instructions, with the rows' activation scales (4-byte DMA).
+// * Each wave streams the weight rows of its own 16 output columns (X1 and X2) into a private
+//   ring.
 // * One barrier per K step: a wave waits for its own DMAs of the step's block (counted vmcnt),
 //   the barrier makes everyone's visible and frees the slot read in the previous step, which is
 //   refilled at once with the block D-1 steps ahead. The prefetch runs across item boundaries
@@ -260,231 +261,6 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
   vm_wait<0>();  // no DMA may still target this workgroup's LDS when it retires
 }
 
-// ---- GEMM2 ------------------------------------------------------------------------------------
-
-template <int MT, int NW>
-struct T2Item {
-  const uint8_t* wbase;  // the expert's W2
-  uint32_t wsoff;        // h0 * I (this wave's first W2 row)
-  LaneScales sc[NW];     // weight scales of this wave's row blocks
-  uint32_t aoff[MT];     // per lane: byte offset of its C DMA chunk (pair row, K 0)
-  float wgt[MT];         // routing weight of the lane's output row in each sub-tile
-  int m0, cnt, seg, h0;
-};
-
-template <int MT, int NW, int D>
-__global__ __launch_bounds__(256) void gemm2_tile_kernel(
-    const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const float* __restrict__ sorted_w, float* __restrict__ partial, int H, int I, int E_l,
-    int max_pairs) {
-  static_assert(D >= 3, "the prefetch lead is D-1 blocks");
-  constexpr int BM = 16 * MT;
-  constexpr int ARow = 2 * kBlock;   // bf16 C bytes per row per K block
-  constexpr int OPS = 2 * NW + MT;   // per wave per step: W2 DMAs + C DMAs (4 rows x 256 B each)
-  constexpr int MW = MT + 2 * NW;    // metadata dwords per lane
-  __shared__ __attribute__((aligned(16))) uint32_t mring[kWaves][MW][kWave];
-  __shared__ __attribute__((aligned(16))) uint8_t bring[kWaves][D][NW * kWBlk];
-  __shared__ __attribute__((aligned(16))) uint8_t aring[D][BM * ARow];
-
-  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
-  const int r16 = lane & 15, g = lane >> 4;
-  const int NNT = H / (64 * NW), NKB = I / kBlock;
-  TileMap tm;
-  tm.init(counts, offsets, E_l, BM);
-  const int items = tm.total * NNT;
-  int it = uniform((int)blockIdx.x);
-  if (it >= items) return;
-  const int stride = gridDim.x;
-
-  const __amdgpu_buffer_rsrc_t cres = make_rsrc(C, (uint32_t)max_pairs * I * 2);
-  const uint32_t dma0 = wblk_dma_off(lane, 0, I), dma1 = wblk_dma_off(lane, 1, I);
-  const uint32_t rd0 = wblk_read_off(lane, 0), rd1 = wblk_read_off(lane, 1);
-  uint8_t* my_bring = &bring[w][0][0];
-
-  // C DMA instruction i of wave w covers tile rows 4*(w*MT + i) + lane/16, 16-byte chunk
-  // position lane & 15 holding chunk (lane & 15) ^ (row & 15). Per-lane metadata (routing
-  // weights of the lane's output rows, weight-scale rows) comes by 4-byte DMA into a per-wave
-  // LDS area and is read back at the item switch.
-  const __amdgpu_buffer_rsrc_t wgtres = make_rsrc(sorted_w, (uint32_t)max_pairs * 4);
-  const __amdgpu_buffer_rsrc_t s2res = make_rsrc(s2, (uint32_t)E_l * (H / kBlock) * NKB * 4);
-  uint32_t* my_meta = &mring[w][0][0];
-  auto meta = [&](int item, T2Item<MT, NW>& x) {
-    item = uniform(item);
-    const int tile = item / NNT, nt = item % NNT;
-    const int e = tm.find(tile, BM, x.m0, x.cnt, x.seg);
-    x.m0 = uniform(x.m0);
-    x.cnt = uniform(x.cnt);
-    x.seg = uniform(x.seg);
-    x.h0 = uniform(nt * 64 * NW + w * 16 * NW);
-    x.wbase = uniform(w2 + (size_t)e * H * I);
-    x.wsoff = uniform((uint32_t)x.h0 * I);
-    const int last = x.cnt - 1;
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int row = 4 * (w * MT + i) + (lane >> 4);
-      const int r = x.m0 + row;
-      x.aoff[i] = ((uint32_t)(x.seg + (r < last ? r : last)) * I) * 2 +
-                  16 * ((lane & 15) ^ (row & 15));
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = x.m0 + mt * 16 + r16;
-      dma4(wgtres, my_meta + mt * kWave, 4u * (x.seg + (r < last ? r : last)), 0);
-    }
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      const uint32_t so = uniform(
-          (uint32_t)(((size_t)e * (H / kBlock) + (x.h0 + 16 * j) / kBlock) * NKB) * 4);
-      dma4(s2res, my_meta + (MT + 2 * j) * kWave, 4u * lane, so);
-      dma4(s2res, my_meta + (MT + 2 * j + 1) * kWave, 4u * (lane + kWave), so);
-    }
-  };
-  auto finish = [&](T2Item<MT, NW>& x) {
-    const uint32_t mb = lds_addr(my_meta) + 4 * lane;
-    float v[MW];
-#pragma unroll
-    for (int j = 0; j < MW; ++j) v[j] = ds_read4f(mb + j * 4 * kWave);
-    lds_wait_all();
-#pragma unroll
-    for (int j = 0; j < MW; ++j) lds_fence(v[j]);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) x.wgt[mt] = v[mt];
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      x.sc[j].v0 = v[MT + 2 * j];
-      x.sc[j].v1 = v[MT + 2 * j + 1];
-    }
-  };
-
-  T2Item<MT, NW> cur, nxt, nn;
-  meta(it, cur);
-  vm_wait<0>();
-  finish(cur);
-  int it_n = it + stride;
-  meta(it_n < items ? it_n : it, nxt);
-  vm_wait<0>();
-  finish(nxt);
-
-  auto issue = [&](bool second, int kbi, int slot) {
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-      dma16(cres, &aring[slot][(w * MT + i) * 1024], second ? nxt.aoff[i] : cur.aoff[i],
-            (uint32_t)kbi * ARow);
-    const __amdgpu_buffer_rsrc_t wres =
-        make_rsrc(uniform(second ? nxt.wbase : cur.wbase), (uint32_t)H * I);
-    const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
-    uint8_t* b = my_bring + slot * NW * kWBlk;
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      dma16(wres, b + j * kWBlk, dma0, ws + (uint32_t)j * 16 * I);
-      dma16(wres, b + j * kWBlk + 1024, dma1, ws + (uint32_t)j * 16 * I);
-    }
-  };
-
-#pragma unroll
-  for (int d = 0; d < D - 1; ++d) {
-    issue(false, d, d);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  int slot = 0;  // ring slot of the next block to compute (a running step count mod D)
-  for (;;) {
-    const int it_nn = it_n + stride;
-    meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
-
-    v4f acc[MT][NW];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int j = 0; j < NW; ++j) acc[mt][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    int kb = 0;
-    do {
-      {
-        const int d = slot;
-        vm_wait<vm_depth((D - 2) * OPS)>();
-        __builtin_amdgcn_s_barrier();
-        const int kn = kb + D - 1;
-        const bool second = kn >= NKB;
-        issue(second, second ? kn - NKB : kn, d == 0 ? D - 1 : d - 1);
-        __builtin_amdgcn_sched_barrier(0);
-
-        const uint32_t bb = lds_addr(my_bring + d * NW * kWBlk);
-        const uint32_t ab = lds_addr(&aring[d][0]);
-        v4u wl[NW], wh[NW];
-#pragma unroll
-        for (int j = 0; j < NW; ++j) {
-          wl[j] = ds_read16(bb + j * kWBlk + rd0);
-          wh[j] = ds_read16(bb + j * kWBlk + rd1);
-        }
-        v4u a[MT][4];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int row = mt * 16 + r16;
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            a[mt][c] = ds_read16(ab + row * ARow + 16 * ((4 * g + c) ^ (row & 15)));
-        }
-        lds_wait_all();
-        v8bf bw[NW][4];
-#pragma unroll
-        for (int j = 0; j < NW; ++j) {
-          lds_fence(wl[j]);
-          lds_fence(wh[j]);
-          const uint32_t wv[8] = {wl[j][0], wl[j][1], wl[j][2], wl[j][3],
-                                  wh[j][0], wh[j][1], wh[j][2], wh[j][3]};
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            v2bf p0, p1, p2, p3;
-            fp8x4_to_bf16x4((int)wv[2 * c], p0, p1);
-            fp8x4_to_bf16x4((int)wv[2 * c + 1], p2, p3);
-            bw[j][c] = v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-          }
-        }
-        float sw[NW];
-#pragma unroll
-        for (int j = 0; j < NW; ++j) sw[j] = cur.sc[j].get(kb);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) lds_fence(a[mt][c]);
-#pragma unroll
-          for (int j = 0; j < NW; ++j) {
-            v4f t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              t = mfma_bf16_16x16x32(bw[j][c], __builtin_bit_cast(v8bf, a[mt][c]), t);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mt][j][i] = fmaf(t[i], sw[j], acc[mt][j][i]);
-          }
-        }
-      }
-      slot = slot + 1 == D ? 0 : slot + 1;
-      ++kb;
-    } while (kb < NKB);
-    vm_wait<vm_depth((D - 1) * OPS)>();
-    finish(nn);
-
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = cur.m0 + mt * 16 + r16;
-      if (r < cur.cnt) {
-        const float wp = cur.wgt[mt];
-        float* orow = partial + (size_t)(cur.seg + r) * H + cur.h0 + 4 * g;
-#pragma unroll
-        for (int j = 0; j < NW; ++j)
-          *(float4*)(orow + 16 * j) = float4{acc[mt][j][0] * wp, acc[mt][j][1] * wp,
-                                             acc[mt][j][2] * wp, acc[mt][j][3] * wp};
-      }
-    }
-    if (it_n >= items) break;
-    it = it_n;
-    it_n = it_nn;
-    cur = nxt;
-    nxt = nn;
-  }
-  vm_wait<0>();
-}
-
 }  // namespace
 
 static int tile_grid(int per_cu, long long max_items) {
@@ -504,17 +280,10 @@ static inline long long tile_count(int max_pairs, int bm, int E_l) {
   return (max_pairs + bm - 1) / bm + (E_l < max_pairs ? E_l : max_pairs);
 }
 
-#ifndef JG_G2T_NW
-#define JG_G2T_NW 1
-#endif
-
 // Ring depths (lead D-1 blocks). D = 3 keeps two workgroups per CU within the 160 KiB of LDS,
 // which measured faster than deeper rings at one workgroup per CU.
 #ifndef JG_G1T_D
 #define JG_G1T_D 3
-#endif
-#ifndef JG_G2T_D
-#define JG_G2T_D 3
 #endif
 
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
@@ -536,27 +305,6 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
   if (mt <= 4) JG_G1T(4, JG_G1T_D)
   JG_G1T(8, (JG_G1T_D > 4 ? 4 : JG_G1T_D))  // a 128-row tile leaves room for 4 slots
 #undef JG_G1T
-}
-
-hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* s2,
-                             const int32_t* counts, const int32_t* offsets,
-                             const float* sorted_w, float* partial, int H, int I, int E_l,
-                             int max_pairs, int mt, hipStream_t stream) {
-#define JG_G2T(MT, NW, D)                                                                        \
-  {                                                                                              \
-    if (I / kBlock < (D) - 1) return hipErrorNotSupported; /* lead must stay within one item */  \
-    constexpr int lds = kWaves * D * NW * kWBlk + D * 16 * MT * 2 * kBlock +                     \
-                        kWaves * (MT + 2 * NW) * kWave * 4;                                      \
-    const int grid = tile_grid(tile_groups_per_cu(lds),                                          \
-                               tile_count(max_pairs, 16 * MT, E_l) * (H / (64 * NW)));           \
-    gemm2_tile_kernel<MT, NW, D><<<grid, kWaves * kWave, 0, stream>>>(                           \
-        C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs);                    \
-    return hipGetLastError();                                                                    \
-  }
-  // BM is capped at 64 here: a 128-row bf16 ring would not fit next to the weight rings.
-  if (mt <= 2) JG_G2T(2, JG_G2T_NW, JG_G2T_D)
-  JG_G2T(4, JG_G2T_NW, JG_G2T_D)
-#undef JG_G2T
 }
 
 }  // namespace jgmoe

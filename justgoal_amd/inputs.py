@@ -47,6 +47,15 @@ CONFIGS = {
     "ds_t16384_skew": Config("ds_t16384_skew", DS_V3, 16384, skew_experts=8, skew_offset=3.0,
                              seed=BENCH_SEED),
     "qwen3_t1024": Config("qwen3_t1024", QWEN3, 1024, seed=BENCH_SEED),
+    "qwen3_t128": Config("qwen3_t128", QWEN3, 128, seed=BENCH_SEED),
+    "qwen3_t512": Config("qwen3_t512", QWEN3, 512, seed=BENCH_SEED),
+    # prefill chunks between the decode and the large-batch cases (LDS-tile kernels)
+    "ds_t128": Config("ds_t128", DS_V3, 128, seed=BENCH_SEED),
+    "ds_t256": Config("ds_t256", DS_V3, 256, seed=BENCH_SEED),
+    "ds_t512": Config("ds_t512", DS_V3, 512, seed=BENCH_SEED),
+    "ds_t768": Config("ds_t768", DS_V3, 768, seed=BENCH_SEED),
+    "ds_t1024": Config("ds_t1024", DS_V3, 1024, seed=BENCH_SEED),
+    "ds_t2048": Config("ds_t2048", DS_V3, 2048, seed=BENCH_SEED),
 }
 
 
