@@ -97,7 +97,14 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 
 // M sub-tiles (of 16 rows) per work item for an expected segment length.
 static inline int stream_mt(int rows_hint) { return rows_hint <= 16 ? 1 : rows_hint <= 32 ? 2 : 4; }
-static inline int tile_mt(int rows_hint) { return rows_hint <= JG_TILE_MT8_ROWS ? 4 : 8; }
+// LDS-tiled GEMM1 tile height: 32 rows up to 16 expected rows per expert (T=256: 122.8 ->
+// 116.7 us), 64 above (128-row tiles measured far slower at 32: 239 vs 158 us).
+#ifndef JG_TILE_MT2_ROWS
+#define JG_TILE_MT2_ROWS 16
+#endif
+static inline int tile_mt(int rows_hint) {
+  return rows_hint <= JG_TILE_MT2_ROWS ? 2 : rows_hint <= JG_TILE_MT8_ROWS ? 4 : 8;
+}
 
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                         const float* s13, const int32_t* counts, const int32_t* offsets,

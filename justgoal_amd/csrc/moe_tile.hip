@@ -59,7 +59,10 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
   __shared__ __attribute__((aligned(16))) uint32_t mring[kWaves][MW][kWave];
   __shared__ __attribute__((aligned(16))) uint8_t bring[kWaves][D][2 * kWBlk];
   __shared__ __attribute__((aligned(16))) uint8_t aring[D][BM * kBlock];
-  __shared__ __attribute__((aligned(16))) float sring[D][BM];
+  // Each wave's scale DMA writes 64 dwords (one per lane) from row (w*64) mod BM, so a slot
+  // holds at least 64 floats even when BM = 32 (lanes past the tile repeat its last row).
+  constexpr int SROW = BM < kWave ? kWave : BM;
+  __shared__ __attribute__((aligned(16))) float sring[D][SROW];
 
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int r16 = lane & 15, g = lane >> 4;
@@ -293,8 +296,8 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
 #define JG_G1T(MT, D)                                                                           \
   {                                                                                             \
     if (H / kBlock < (D) - 1) return hipErrorNotSupported; /* lead must stay within one item */ \
-    constexpr int lds = kWaves * D * 2 * kWBlk + D * 16 * MT * kBlock + D * 16 * MT * 4 +      \
-                        kWaves * (MT / 2 + 5) * kWave * 4;                                       \
+    constexpr int lds = kWaves * D * 2 * kWBlk + D * 16 * MT * kBlock +                         \
+                        D * (MT < 4 ? kWave : 16 * MT) * 4 + kWaves * (MT / 2 + 5) * kWave * 4;  \
     const int grid =                                                                            \
         tile_grid(tile_groups_per_cu(lds), tile_count(max_pairs, 16 * MT, E_l) * (I / 64));     \
     gemm1_tile_kernel<MT, D><<<grid, kWaves * kWave, 0, stream>>>(                              \

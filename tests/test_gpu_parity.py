@@ -106,8 +106,18 @@ def check_case(geom, T, device, seed=0, tokens_checked=None, local_offset=0, bia
     err = (got.float() - ref.float()).abs()
     tol = ATOL + RTOL * ref.float().abs()
     bad = int((err > tol).sum())
-    say(f"  pairs={n} max_abs_err={float(err.max()):.3e} n_bad={bad} of {err.numel()}")
+    # Consistency bar next to the tolerance: the kernels differ from the oracle only by fp32
+    # accumulation order and one bf16 rounding, so outputs off by more than 2^-6 of their own
+    # size plus their token row's mean size are rare cancellations (sums much larger than the
+    # result) or wrong data: at most 1 in 10^4 may (the absolute 2e-2 alone passes wrong results
+    # wherever outputs are of order 0.03; a mis-staged scale put 25-35% of them past this bar).
+    mag = ref.float().abs()
+    strict = int((err > 2.0 ** -6 * (mag + mag.mean(dim=1, keepdim=True))).sum())
+    strict_allowed = max(2, err.numel() // 10000)
+    say(f"  pairs={n} max_abs_err={float(err.max()):.3e} n_bad={bad} n_strict={strict} "
+        f"of {err.numel()}")
     torch.testing.assert_close(got.float(), ref.float(), rtol=RTOL, atol=ATOL)
+    assert strict <= strict_allowed, f"{strict} outputs off by more than 2^-6 of their scale"
     return out, ws
 
 
