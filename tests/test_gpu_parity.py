@@ -375,7 +375,7 @@ def random_geometries(n, seed=2024, large=False):
     return out
 
 
-@pytest.mark.parametrize("case", random_geometries(24) + random_geometries(8, 77, large=True),
+@pytest.mark.parametrize("case", random_geometries(64) + random_geometries(32, 77, large=True),
                          ids=lambda c: f"{c[0].name}-T{c[1]}")
 def test_random_geometries(gpu, case):
     geom, T, off, bias = case
