@@ -53,6 +53,11 @@ __device__ __forceinline__ int xcd_item(int i, int items) {
 
 constexpr int vm_depth(int n) { return n > 63 ? 63 : n < 0 ? 0 : n; }
 
+// 16-byte chunk permutation of row n of the GEMM2 C tile in LDS (256-byte bf16 rows, one K
+// block; depends on n mod 16). The fragment read (lane = row n | group g, chunks 4g..4g+3) took
+// 21% less time with this permutation than with n & 15 in a ds_read_b128 probe.
+__device__ __forceinline__ int crow_swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
+
 // ---- GEMM1 ------------------------------------------------------------------------------------
 //
 // Five waves: waves 0..3 compute (2x2 grid over the BM x BN tile), wave 4 is the producer that
@@ -473,14 +478,14 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
   if (w == kProducer) {
     const uint32_t dma0 = wblk_dma_off(lane, 0, I), dma1 = wblk_dma_off(lane, 1, I);
     // C DMA instruction j covers tile rows 4j + lane/16, chunk position lane & 15 holding
-    // chunk (lane & 15) ^ (row & 15). The offsets are relative to the tile's first row and the
+    // chunk (lane & 15) ^ crow_swz(row). The offsets are relative to the tile's first row and the
     // same for every item: each item's buffer resource starts at that row and ends at the
     // segment's last row, so rows past the segment are out of range (never fetched).
     uint32_t aoff[AI];
 #pragma unroll
     for (int j = 0; j < AI; ++j) {
       const int row = 4 * j + (lane >> 4);
-      aoff[j] = (uint32_t)row * I * 2 + 16 * ((lane & 15) ^ (row & 15));
+      aoff[j] = (uint32_t)row * I * 2 + 16 * ((lane & 15) ^ crow_swz(row));
     }
     B2Scalars cur, nxt, nn;
     scalars(it, cur);
@@ -590,7 +595,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
   auto read_a = [&](uint32_t ab, int ms, v4u(&x)[4]) {
     const int row = (wm * MS + ms) * 16 + r16;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) x[c] = ds_read16(ab + row * ARow + 16 * ((4 * g + c) ^ (row & 15)));
+    for (int c = 0; c < 4; ++c) x[c] = ds_read16(ab + row * ARow + 16 * ((4 * g + c) ^ crow_swz(row)));
   };
   auto read_head = [&](int d) {
     const uint32_t bb = lds_addr(&bring[d][0]) + wn * NS * kWBlk;
