@@ -36,6 +36,10 @@ PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
 PEAK_BF16_TFLOPS = 2500.0
 STAGES = ("route", "permute", "gemm1_swiglu", "gemm2", "combine")
+# GEMM1 kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (JG_STREAM_MAX_ROWS,
+# JG_BIG_ROWS defaults; tests/test_bench.py checks they match the source)
+GEMM1_STREAM_MAX_ROWS = 4
+GEMM1_BIG_ROWS = 64
 
 
 def log(msg):
@@ -152,12 +156,12 @@ def measure_quant(T, H, steps, warmup, dev):
 
 def gemm1_kernel_name(cfg):
     """The GEMM1+SwiGLU kernel family the library picks for this shape: the shape-only rule of
-    justgoal_amd/csrc/moe_gemm.hip (expected pairs per expert T*top_k/E: <= 16 streaming,
-    >= 64 large tiles, else LDS tiles)."""
+    justgoal_amd/csrc/moe_gemm.hip (expected pairs per expert T*top_k/E: <= GEMM1_STREAM_MAX_ROWS
+    streaming, >= GEMM1_BIG_ROWS large tiles, else LDS tiles)."""
     g = cfg.geom
     rows = cfg.tokens * g.top_k // g.num_experts
-    return ("gemm1_stream_kernel" if rows <= 16 else
-            "gemm1_tile_kernel" if rows < 64 else "gemm1_big_kernel")
+    return ("gemm1_stream_kernel" if rows <= GEMM1_STREAM_MAX_ROWS else
+            "gemm1_tile_kernel" if rows < GEMM1_BIG_ROWS else "gemm1_big_kernel")
 
 
 def load_traffic(name):

@@ -49,3 +49,16 @@ def test_routing_stats_read_the_given_workspace():
     v["pair_of"][5, 0] = 1
     v["pair_of"][5, 7] = 2
     assert bench.routing_stats(DS_V3, T, ws) == (3, 2, 2)
+
+
+def test_kernel_family_thresholds_match_the_library_source():
+    import re
+    src = open(os.path.join(ROOT, "justgoal_amd", "csrc", "moe_gemm.hip")).read()
+    stream = int(re.search(r"#define JG_STREAM_MAX_ROWS (\d+)", src).group(1))
+    big = int(re.search(r"#define JG_BIG_ROWS (\d+)", src).group(1))
+    assert (bench.GEMM1_STREAM_MAX_ROWS, bench.GEMM1_BIG_ROWS) == (stream, big)
+    from justgoal_amd import inputs as jin
+    names = {n: bench.gemm1_kernel_name(c) for n, c in jin.CONFIGS.items()}
+    assert names["ds_t64"] == "gemm1_stream_kernel"
+    assert names["ds_t512"] == "gemm1_tile_kernel"
+    assert names["ds_t4096"] == "gemm1_big_kernel"
