@@ -92,3 +92,46 @@ def test_token_limit_rejected_on_host():
 def test_zero_tokens_is_a_no_op():
     # T = 0: nothing to enqueue, success without a device
     assert _lib.lib().moe_run(*([None] * 8), 0, 2.5, None, None, 0, None) == 0
+
+
+def test_other_entry_points_validate_on_host():
+    """Routing-only, quantisation, layout and stage-hook entry points reject bad arguments before
+    touching a device, and T = 0 is a no-op everywhere."""
+    L = _lib.lib()
+    g = DS_V3.c_struct()
+    bad = Geometry(7100, 2048, 256, 32, 8, 8, 4, ROUTING_DS).c_struct()
+    # moe_route_ex
+    assert L.moe_route_ex(ctypes.byref(bad), 1, 1, 0, 2.5, 1, 16, None) == -2
+    assert L.moe_route_ex(ctypes.byref(g), 1, 1, 0, 2.5, 1, -1, None) == -1
+    assert L.moe_route_ex(ctypes.byref(g), None, 1, 0, 2.5, 1, 16, None) == -1
+    assert L.moe_route_ex(ctypes.byref(g), 1, 1, 0, 2.5, None, 16, None) == -1
+    assert L.moe_route_ex(ctypes.byref(g), None, None, 0, 2.5, None, 0, None) == 0
+    # moe_quantize_activations
+    assert L.moe_quantize_activations(1, -1, 7168, 1, 1, None) == -1
+    assert L.moe_quantize_activations(1, 4, 7100, 1, 1, None) == -1
+    assert L.moe_quantize_activations(1, 4, 0, 1, 1, None) == -1
+    assert L.moe_quantize_activations(None, 4, 7168, 1, 1, None) == -1
+    assert L.moe_quantize_activations(1, 4, 7168, None, 1, None) == -1
+    assert L.moe_quantize_activations(1, 4, 7168, 1, None, None) == -1
+    assert L.moe_quantize_activations(None, 0, 7168, None, None, None) == 0
+    # moe_workspace_layout / moe_workspace_bytes_ex
+    offs = (ctypes.c_int64 * (_lib.MOE_WS_NUM_REGIONS + 1))()
+    assert L.moe_workspace_layout(ctypes.byref(bad), 16, offs) == -2
+    assert L.moe_workspace_layout(ctypes.byref(g), -1, offs) == -1
+    assert L.moe_workspace_layout(ctypes.byref(g), 16, None) == -1
+    assert L.moe_workspace_bytes_ex(ctypes.byref(g), -1) == -1
+    # moe_set_stage_events: off with n = 0; otherwise exactly MOE_NUM_STAGES + 1 non-null events
+    assert L.moe_set_stage_events(None, 0) == 0
+    assert L.moe_set_stage_events(None, 6) == -1
+    ev = (ctypes.c_void_p * 6)(*([1] * 5 + [None]))
+    assert L.moe_set_stage_events(ev, 6) == -1
+    assert L.moe_set_stage_events(ev, 3) == -1
+    assert L.moe_set_stage_events(None, 0) == 0
+
+
+def test_error_strings():
+    L = _lib.lib()
+    assert L.moe_error_string(0).decode() == "success"
+    for rc, word in ((-1, "argument"), (-2, "geometry"), (-3, "gfx950")):
+        assert word in L.moe_error_string(rc).decode()
+    assert L.moe_error_string(-99).decode() == "unknown error"
