@@ -43,6 +43,10 @@ constexpr int kWBlk = 16 * kBlock;  // one weight K-block image: 16 rows x 128 b
 // vmcnt holds 6 bits; deeper counts are clamped, which only makes a wait stricter.
 constexpr int vm_depth(int n) { return n > 63 ? 63 : n; }
 
+// A per-lane buffer offset past every buffer these kernels address (the API keeps each below
+// 2^31 - 16): loads with it return zeros without a memory access.
+constexpr uint32_t kNoFetch = 0x7ffffff0u;
+
 // ---- GEMM1: C = SwiGLU(A W1^T, A W3^T) --------------------------------------------------------
 
 template <int MT>
@@ -125,23 +129,27 @@ __global__ __launch_bounds__(256) void gemm1_stream_kernel(
   finish(nxt, tok);
 
   G1Slot<MT> sl[D];
-  // Issue K block kbi of item cur (or nxt when `second`) into slot d.
+  // Issue K block kbi of item cur (or nxt when `second`) into slot d. After a wave's last item
+  // there is no next item: those prefetches keep the step's operation count (the counted waits
+  // rely on it) but use an out-of-range offset, so they return zeros and fetch nothing.
   auto issue = [&](bool second, int kbi, G1Slot<MT>& s, int d) {
+    const bool dead = uniform(second && it_n >= items);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const uint32_t ao = second ? nxt.aoff[mt] : cur.aoff[mt];
-      const uint32_t so = second ? nxt.saoff[mt] : cur.saoff[mt];
+      const uint32_t ao = dead ? kNoFetch : second ? nxt.aoff[mt] : cur.aoff[mt];
+      const uint32_t so = dead ? kNoFetch : second ? nxt.saoff[mt] : cur.saoff[mt];
       s.a[mt] = buf_load32(ares, ao, (uint32_t)kbi * kBlock);
       s.sa[mt] = __uint_as_float(buf_load32b(sares, so, (uint32_t)kbi * T * 4));
     }
     const __amdgpu_buffer_rsrc_t wres =
         make_rsrc(uniform(second ? nxt.wbase : cur.wbase), 2u * I * H);
     const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
+    const uint32_t w0 = dead ? kNoFetch : dma0, w1 = dead ? kNoFetch : dma1;
     uint8_t* slot = my_ring + d * 2 * kWBlk;
-    dma16(wres, slot, dma0, ws);
-    dma16(wres, slot + 1024, dma1, ws);
-    dma16(wres, slot + kWBlk, dma0, ws + (uint32_t)I * H);
-    dma16(wres, slot + kWBlk + 1024, dma1, ws + (uint32_t)I * H);
+    dma16(wres, slot, w0, ws);
+    dma16(wres, slot + 1024, w1, ws);
+    dma16(wres, slot + kWBlk, w0, ws + (uint32_t)I * H);
+    dma16(wres, slot + kWBlk + 1024, w1, ws + (uint32_t)I * H);
   };
 
   // Prologue in issue order: the loop's wait counts assume every slot's loads went out
@@ -307,14 +315,16 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
   meta(it_n < items ? it_n : it, nxt);
 
   G2Slot<MT> sl[D];
+  // As in GEMM1, prefetches past a wave's last item use an out-of-range offset (no traffic).
   auto issue = [&](bool second, int kbi, G2Slot<MT>& s, int d) {
+    const bool dead = uniform(second && it_n >= items);
     const __amdgpu_buffer_rsrc_t cr =
         JG_G2S_BOUNDED ? make_rsrc(uniform(second ? nxt.cbase : cur.cbase),
                                    uniform(second ? nxt.crec : cur.crec))
                        : cres;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const uint32_t co = second ? nxt.coff[mt] : cur.coff[mt];
+      const uint32_t co = dead ? kNoFetch : second ? nxt.coff[mt] : cur.coff[mt];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         s.a[mt][c] = JG_ABL_NOC ? uint4{0, 0, 0, 0} : buf_load16(cr, co, 2 * (kbi * kBlock + 8 * c));
@@ -323,8 +333,8 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
         make_rsrc(uniform(second ? nxt.wbase : cur.wbase), (uint32_t)H * I);
     const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
     uint8_t* slot = my_ring + d * kWBlk;
-    dma16(wres, slot, dma0, ws);
-    dma16(wres, slot + 1024, dma1, ws);
+    dma16(wres, slot, dead ? kNoFetch : dma0, ws);
+    dma16(wres, slot + 1024, dead ? kNoFetch : dma1, ws);
   };
 
   // Prologue in issue order: the loop's wait counts assume every slot's loads went out
