@@ -1,22 +1,23 @@
-// Large-tile grouped GEMMs for long per-expert segments (prefill-sized batches).
+// Large-tile grouped GEMMs for long per-expert segments (prefill-sized and skewed batches; GEMM2
+// also for a few pairs per expert, where its padding-row skip keeps part-filled tiles cheap).
 //
-// A workgroup of four waves in a 2x2 grid computes a BM x BN output tile of one expert: each wave
-// owns (BM/2) x (BN/2). Both operands reach LDS by DMA into rings of D slots shared by the four
-// waves, so every weight K-block is fetched once per BM rows (not once per 16 columns per wave as
-// in the smaller tiles) and every activation K-block once per BN columns:
+// A workgroup (one per CU) computes a 128 x 128 output tile of one expert with eight compute
+// waves (GEMM1: 2x4 grid, wave tile 64 rows x 32 C columns; GEMM2: 4x2, 32 rows x 64 H columns)
+// and one producer wave. Both operands reach LDS by DMA into a 3-slot ring, so every weight
+// K-block is fetched once per 128 rows and every activation K-block once per 128 columns:
 //
-// * GEMM1: BM rows of fp8 hidden states (gathered from the token rows) plus their activation
-//   scales, and BN columns of C, i.e. BN X1 rows and BN X2 rows of W13. The epilogue applies
-//   SwiGLU and stores bf16 C.
-// * GEMM2: BM rows of bf16 C and BN rows of W2; the epilogue scales by the pair's routing weight
-//   and stores fp32 rows for the combine.
+// * GEMM1: 128 rows of fp8 hidden states (gathered through the pair -> token list) plus their
+//   activation scales, and 128 columns of C, i.e. 128 X1 rows and 128 X2 rows of W13. The
+//   epilogue applies SwiGLU and stores bf16 C.
+// * GEMM2: 128 rows of bf16 C and 128 rows of W2; the epilogue scales by the pair's routing
+//   weight and stores fp32 rows for the combine.
 //
-// Per K step: each wave waits for its own DMAs of the step's block (counted vmcnt), one bare
-// s_barrier makes all of them visible and frees the slot read in the previous step, the slot is
-// refilled with the block D-1 steps ahead (across item boundaries; the next item's per-lane
-// metadata arrives by 4-byte DMA in a per-wave LDS area), then the wave reads its MFMA fragments
-// from LDS and runs (BM/32)*(BN/32) fragment products per matrix. LDS images use the XOR chunk
-// swizzle of the other kernels; MFMA forms and scale handling are those of moe_tile.hip.
+// Per K step the producer waits for its own DMAs of the step's block (counted vmcnt), passes the
+// workgroup barrier and refills the slot freed by the previous step with the block two steps
+// ahead (across item boundaries). The compute waves never touch vector memory in the K loop:
+// they read their MFMA fragments from LDS, the next block's first fragments under the current
+// block's last MFMAs, with the barrier placed between those two halves. LDS images use XOR
+// chunk swizzles chosen for conflict-free ds_read_b128 fragment reads.
 #include "moe_device.h"
 #include "moe_kernels.h"
 

@@ -16,7 +16,8 @@
 //   rows) is resolved one item ahead so no load is waited on at an item switch.
 // * All waits are counted: each K step issues the same number of vector-memory operations, so
 //   "slot d is complete" is vmcnt <= (D-1) * ops_per_step. Blocks past the end of the wave's
-//   last item re-read that item's data and are never used.
+//   last item are still issued (to keep that count) but with an out-of-range offset, so they
+//   return zeros without fetching anything.
 //
 // MFMA form: weights are the first operand, so lane l holds output column 4*(l>>4)+i for row
 // (pair) l & 15. GEMM1 applies the activation scale (one per lane) times the weight scale of the
