@@ -1,24 +1,17 @@
-// Grouped expert GEMMs and the weighted combine.
+// Kernel selection for the two expert GEMMs, and the weighted combine.
 //
-// GEMM1 (W13) + SwiGLU. For one M-tile of an expert's segment (BM = 16*MT pairs) and 64*NW
-// columns of C, each wave owns NW column tiles of 16 in both halves of W13 (X1 rows c, X2 rows
-// I + c), so the SwiGLU epilogue pairs accumulators that sit in the same lane and register.
-// K runs over H in 128-wide scale blocks; one v_mfma_f32_16x16x128_f8f6f4 covers a block exactly,
-// its fp32 result is scaled by hs_scale[kb, token] * s13[e, n/128, kb] and added to the running
-// accumulator (reference: goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:125-132).
-// C is kept in bf16 (not requantised to fp8 as the reference solutions do at main.py:151-156).
+// The GEMMs themselves live in moe_stream.hip (weight streaming, a few pairs per expert),
+// moe_tile.hip (LDS-tiled GEMM1) and moe_big.hip (large tiles). Their arithmetic is the same:
+// GEMM1 runs one v_mfma_f32_16x16x128_f8f6f4 per 128-wide K scale block and adds its fp32 result
+// times hs_scale[kb, token] * s13[e, n/128, kb] to the accumulator
+// (goal_full_shape/opus-4.8/moe_fp8_fwd/MOEDIR/main.py:125-132), then applies SwiGLU into bf16 C
+// (not requantised to fp8 as the reference solutions do at main.py:151-156); GEMM2 converts the
+// W2 e4m3 bytes to bf16 exactly, runs four v_mfma_f32_16x16x32_bf16 per K block (lane group
+// g = lane>>4 carries K = 32g + 8c .. +8 for instruction c, the same map on both operands), scales
+// by s2[e, h/128, kb] and writes fp32 rows times the pair's routing weight.
 //
-// GEMM2 (W2). Same tiling over (pairs x H); C rows are bf16, W2 e4m3 bytes are converted to bf16
-// in registers (exact) and fed to v_mfma_f32_16x16x32_bf16; each 128-wide K block is scaled by
-// s2[e, h/128, kb]. The epilogue multiplies by the pair's routing weight and stores fp32 rows.
-//
-// Operands stream straight from HBM into registers (weights are read once per M-tile, so the
-// LDS would only add a hop); a register double buffer keeps one K block of loads in flight.
-//
-// K mapping: within a 128-wide K block, lane group g = lane>>4 holds the 32 contiguous K values
-// [32g, 32g+32) of its row for both operands. For the bf16 MFMA (K=32 per instruction) chunk c
-// of those 32 values is fed to instruction c, so instruction c covers K = {32g + 8c .. +8 : g}.
-// Because A and B use the same map, each output still sums over every K exactly once.
+// The choice of kernel family depends only on shapes (never on routed counts, which stay on the
+// device): see launch_gemm1 / launch_gemm2 below.
 #include <mutex>
 
 #include "moe_device.h"
