@@ -102,7 +102,8 @@ enum {
   MOE_WS_SORTED_W,       /* fp32  [Npmax]     routing weight of each pair */
   MOE_WS_C,              /* bf16  [Npmax, I]  SwiGLU activations */
   MOE_WS_PARTIAL,        /* fp32  [Npmax, H]  weighted GEMM2 rows */
-  MOE_WS_CHUNK_COUNTS,   /* int32 [ceil(T/16), E_l] pairs per local expert per 16-token group */
+  MOE_WS_CHUNK_COUNTS,   /* int32 [ceil(T/c), E_l] pairs per local expert per c-token group,
+                            c = 4 for T <= 256, else 16 (one row per routing workgroup) */
   MOE_WS_NUM_REGIONS     /* total size is written at this index */
 };
 

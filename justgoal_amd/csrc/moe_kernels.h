@@ -21,7 +21,8 @@ hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, const in
                           int32_t* offsets, int32_t* sorted_tok, float* sorted_w,
                           int32_t* pair_of, hipStream_t stream);
 
-// Number of routing workgroups (16 tokens each) = rows of the chunk count table.
+// Number of routing workgroups (4 tokens each up to T = 256, 16 above) = rows of the chunk count
+// table.
 int route_chunks(int T);
 
 // Grouped GEMM1 (W13) with the SwiGLU epilogue: C[p, :] = bf16(X1 * silu(X2)) for every pair p.
