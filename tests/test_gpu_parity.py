@@ -383,3 +383,29 @@ def test_random_geometries(gpu, case):
         f"El={geom.local_experts} K={geom.top_k} groups={geom.n_group}/{geom.topk_group} "
         f"method={geom.routing_method} rows_hint={T * geom.top_k // geom.num_experts}")
     check_case(geom, T, gpu, seed=T, local_offset=off, bias=bias)
+
+
+# The routing-only entry point (moe_route_ex) on its own, at the model geometries: both routing
+# methods, a ragged T on each side of the routing workgroup switch, a full-size batch, and an EP
+# rank's expert window; every returned region is compared bit for bit with the oracle.
+@pytest.mark.parametrize("geom,T,off", [(DS_V3, 1, 0), (DS_V3, 257, 32), (DS_V3, 4096, 224),
+                                        (QWEN3, 3, 0), (QWEN3, 1000, 0), (QWEN3, 4096, 0)])
+def test_route_entry_matches_oracle(gpu, geom, T, off):
+    from justgoal_amd.moe import route
+    print(f"route entry: {geom.name} T={T} off={off}", flush=True)
+    g = torch.Generator().manual_seed(T * 31 + off)
+    lg = torch.randn(T, geom.num_experts, generator=g)
+    b = (torch.randn(geom.num_experts, generator=g) * 0.1).to(torch.bfloat16)
+    rsf = 2.5 if geom.routing_method == ROUTING_DS else 1.0
+    v = route(lg.to(gpu), b.to(gpu), off, rsf, geometry=geom)
+    torch.cuda.synchronize()
+    idx, w = oracle.route(lg, b, geom, rsf)
+    np.testing.assert_array_equal(v["topk_idx"].cpu().numpy(), idx)
+    np.testing.assert_array_equal(v["topk_w"].cpu().numpy().view(np.uint32), w.view(np.uint32))
+    p = oracle.permute(idx, w, off, geom.local_experts)
+    for k in ("counts", "offsets", "pair_of"):
+        np.testing.assert_array_equal(v[k].cpu().numpy(), p[k])
+    n = int(p["offsets"][-1])
+    np.testing.assert_array_equal(v["sorted_tok"][:n].cpu().numpy(), p["sorted_tok"])
+    np.testing.assert_array_equal(v["sorted_w"][:n].cpu().numpy().view(np.uint32),
+                                  p["sorted_w"].view(np.uint32))
