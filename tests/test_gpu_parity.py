@@ -409,3 +409,40 @@ def test_route_entry_matches_oracle(gpu, geom, T, off):
     np.testing.assert_array_equal(v["sorted_tok"][:n].cpu().numpy(), p["sorted_tok"])
     np.testing.assert_array_equal(v["sorted_w"][:n].cpu().numpy().view(np.uint32),
                                   p["sorted_w"].view(np.uint32))
+
+
+# The operator captured in a HIP graph (serving loops replay one): the library records no memset
+# or allocation, so each replay over new inputs copied into the captured buffers must equal an
+# eager call on the same inputs bit for bit. T=64 selects the streaming kernels, T=2048 the large
+# tiles (T * top_k / E = 2 and 64).
+@pytest.mark.parametrize("T", [64, 2048])
+def test_graph_replay_matches_eager(gpu, T):
+    say(f"graph replay: mini-DS T={T}")
+    w = weights_for(MINI_DS, gpu)[1]
+    static = to_dev(jin.make_activations(MINI_DS, T, seed=20), gpu)
+    kw = dict(gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2],
+              gemm2_weights_scale=w[3], local_expert_offset=0, routed_scaling_factor=2.5,
+              geometry=MINI_DS)
+    out = torch.empty(T, MINI_DS.hidden, dtype=torch.bfloat16, device=gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(**static, **kw, output=out)  # warm-up: the stream's workspace exists before capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run(**static, **kw, output=out)
+    for seed in (21, 22, 23):
+        fresh = to_dev(jin.make_activations(MINI_DS, T, seed=seed), gpu)
+        for k, v in fresh.items():
+            static[k].copy_(v)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = run(**fresh, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"replay with seed {seed} differs from the eager call"
+    del g
+    release_workspaces()
