@@ -194,8 +194,8 @@ def cpu_baseline(cfg, kw_dev, reps=3):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", default="ds_t64", choices=sorted(jin.CONFIGS))
     ap.add_argument("--secondary", default="ds_t4096")
     ap.add_argument("--sweep", action="store_true", help="also measure ds_t16384_skew and qwen3_t1024")
@@ -241,7 +241,8 @@ def main():
             w = tuple(t.to(dev) for t in jin.make_weights(c.geom, seed=0))
         else:
             w = wts
-        r, _ = measure(c, w, max(5, args.steps // 2), max(2, args.warmup // 2), dev)
+        # The full warm-up count: clocks settle over tens of ms of load, whatever the call length.
+        r, _ = measure(c, w, max(5, args.steps // 4), args.warmup, dev)
         log(f"[bench] {c.name}: {r['ms_per_call']:.4f} ms, {r['tflops']:.2f} TFLOPS, "
             f"{r['gb_s']:.0f} GB/s, stages {r['stage_ms']}")
         secondary.append(r)
