@@ -180,6 +180,13 @@ def test_qwen3_config4_t1024(gpu):
     check_case(QWEN3, 1024, gpu, seed=0, tokens_checked=256)
 
 
+def test_ds_max_tokens(gpu):
+    """The largest batch the C-ABI accepts for this geometry (65535 tokens: the largest grids and
+    workspace); routing is compared over every token, the output on a token subset."""
+    say("max tokens: DS-V3 T=65535")
+    check_case(DS_V3, 65535, gpu, seed=5, tokens_checked=64)
+
+
 @pytest.mark.parametrize("name", ["ds_t64", "ds_t4096", "ds_t16384_skew", "qwen3_t1024"])
 def test_measured_workloads(name, gpu):
     """The exact batches bench.py times (the configs' own seed)."""
