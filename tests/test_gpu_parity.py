@@ -180,6 +180,14 @@ def test_qwen3_config4_t1024(gpu):
     check_case(QWEN3, 1024, gpu, seed=0, tokens_checked=256)
 
 
+# Qwen3 geometry (H=4096, I=1536: 12 K blocks in GEMM2) across the kernel families:
+# T * top_k / E = 0.06 and 0.5 stream weights, 4 and ~19 use the LDS-tiled GEMM1.
+@pytest.mark.parametrize("T", [1, 8, 64, 300])
+def test_qwen3_small_and_mid_batches(gpu, T):
+    say(f"qwen3 T={T}")
+    check_case(QWEN3, T, gpu, seed=T + 11, tokens_checked=min(T, 64))
+
+
 def test_ds_max_tokens(gpu):
     """The largest batch the C-ABI accepts for this geometry (65535 tokens: the largest grids and
     workspace); routing is compared over every token, the output on a token subset."""
