@@ -1,17 +1,21 @@
 """Benchmark of the FP8 block-scale MoE operator on one MI355X.
 
-``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config ds_t64] [--sweep]``
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads a,b,...]``
 
 A step is one call of the operator (routing -> permute -> GEMM1+SwiGLU -> GEMM2 -> combine) on a
-seeded synthetic batch already resident in HBM. The headline workload is the decode-sized DS-V3
-case (T=64); the prefill-sized T=4096 case is measured in the same run and reported under
-``secondary``. ``--sweep`` adds the skewed T=16384 and the Qwen3 T=1024 cases.
+seeded synthetic batch already resident in HBM. Every BASELINE configuration is measured in one
+run: the T=16 plumbing case, the decode-sized T=64 headline, the prefill-sized T=4096 case, the
+skewed T=16384 case and the Qwen3-style T=1024 case. Each workload first runs W warm-up calls and
+then keeps calling for at least ``--settle-ms`` of wall time (clocks settle over tens of ms of
+load, whatever the call length), then times K (at least 20) back-to-back calls between two HIP
+events.
 
 Prints ONE JSON line. ``value`` is TFLOP/s of the headline workload over algorithmic FLOPs
-(6*H*I per local (token, expert) pair, pairs counted from the routing of the run); ``roofline``
-describes the dominant kernel (GEMM1 + SwiGLU) from stage events recorded on the operator's stream;
-``cpu_baseline`` times the CPU oracle (the dequantise-then-fp32 PyTorch-CPU restatement of the
-operator) on the host cores.
+(6*H*I per local (token, expert) pair, pairs counted from the routing of the run). Each workload
+carries a ``roofline`` block for its dominant kernel (the stage with the largest time, from
+events the library records on the operator's stream); the top-level ``roofline`` is the
+headline's. ``cpu_baseline`` times the CPU oracle (the dequantise-then-fp32 PyTorch-CPU
+restatement of the operator) on all host cores.
 """
 from __future__ import annotations
 
@@ -36,10 +40,11 @@ PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
 PEAK_BF16_TFLOPS = 2500.0
 STAGES = ("route", "permute", "gemm1_swiglu", "gemm2", "combine")
-# GEMM1 kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (JG_STREAM_MAX_ROWS,
-# JG_BIG_ROWS defaults; tests/test_bench.py checks they match the source)
+# Kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (JG_STREAM_MAX_ROWS, JG_BIG_ROWS,
+# JG_G2_STREAM_MAX_ROWS defaults; tests/test_bench.py checks they match the source)
 GEMM1_STREAM_MAX_ROWS = 4
 GEMM1_BIG_ROWS = 64
+GEMM2_STREAM_MAX_ROWS = 3
 
 
 def log(msg):
@@ -58,7 +63,8 @@ def routing_stats(geom, T, ws):
 
 
 def algorithmic(geom, T, pairs, active, tok_local):
-    """FLOPs and HBM bytes the operator must move (intermediates excluded)."""
+    """FLOPs and HBM bytes the operator must move (intermediates excluded), and the same for the
+    two expert GEMMs on their own (each with the intermediates it must read or write once)."""
     H, I = geom.hidden, geom.intermediate
     flops = flops_per_pair(geom) * pairs
     bytes_ = active * weight_bytes_per_expert(geom) + T * bytes_per_token(geom) + 2 * geom.num_experts
@@ -69,10 +75,27 @@ def algorithmic(geom, T, pairs, active, tok_local):
     return flops, bytes_, g1_flops, g1_bytes
 
 
-def time_calls(call, steps, warmup, dev):
+def gemm2_algorithmic(geom, pairs, active):
+    """GEMM2 alone: W2 + S2 of active experts, bf16 C rows read once, one bf16 row written per
+    pair (its output or partial row); 2*I*H FLOPs per pair."""
+    H, I = geom.hidden, geom.intermediate
+    w2 = H * I + 4 * (H // BLOCK) * (I // BLOCK)
+    return 2 * I * H * pairs, active * w2 + pairs * I * 2 + pairs * H * 2
+
+
+def settle_and_time(call, steps, warmup, settle_ms, dev):
+    """W warm-up calls, then more calls until ``settle_ms`` of wall time has passed, then
+    ``steps`` back-to-back calls between two events. Returns (ms per call, warm-up calls run)."""
     for _ in range(warmup):
         call()
     torch.cuda.synchronize(dev)
+    n = warmup
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for _ in range(4):
+            call()
+        n += 4
+        torch.cuda.synchronize(dev)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -80,7 +103,11 @@ def time_calls(call, steps, warmup, dev):
         call()
     end.record()
     torch.cuda.synchronize(dev)
-    return start.elapsed_time(end) / steps
+    return start.elapsed_time(end) / steps, n
+
+
+def time_calls(call, steps, warmup, dev):
+    return settle_and_time(call, steps, warmup, 0.0, dev)[0]
 
 
 def stage_times(call, reps, dev):
@@ -109,7 +136,21 @@ def stage_times(call, reps, dev):
     return {s: tot[i] / reps for i, s in enumerate(STAGES)}
 
 
-def measure(cfg, weights_dev, steps, warmup, dev, seed=None):
+def roofline_block(stage, kernel, ms, flops, nbytes, peak_tflops, workload):
+    """Roofline of one kernel: bound by whichever of FLOPs / peak and bytes / HBM peak is
+    larger; ``achieved`` is the algorithmic rate over the kernel's average launch time."""
+    t_mfma = flops / (peak_tflops * 1e12)
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        bound, achieved, peak, unit = "mfma", flops / (ms * 1e-3) / 1e12, peak_tflops, "TFLOP/s"
+    else:
+        bound, achieved, peak, unit = "hbm", nbytes / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    return {"bound": bound, "kernel": kernel, "stage": stage, "achieved": achieved, "peak": peak,
+            "unit": unit, "frac": achieved / peak, "traffic": load_traffic(stage, workload),
+            "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "avg_launch_ms": ms}
+
+
+def measure(cfg, weights_dev, steps, warmup, settle_ms, dev, seed=None):
     geom = cfg.geom
     seed = cfg.seed if seed is None else seed
     act = jin.make_activations(geom, cfg.tokens, seed=seed, device=dev,
@@ -119,24 +160,28 @@ def measure(cfg, weights_dev, steps, warmup, dev, seed=None):
               gemm2_weights_scale=s2, local_expert_offset=0,
               routed_scaling_factor=2.5 if geom.routing_method == 0 else 1.0)
     call = bind(**kw, geometry=geom)
-    ms = time_calls(call, steps, warmup, dev)
-    st = stage_times(call, max(5, min(steps, 20)), dev)
+    ms, n_warm = settle_and_time(call, steps, warmup, settle_ms, dev)
+    st = stage_times(call, min(steps, 20), dev)
     pairs, active, tok_local = routing_stats(geom, cfg.tokens, call.workspace)
     if pairs == 0:
         raise RuntimeError(f"{cfg.name}: no routed pairs read back from the call's workspace")
     flops, bytes_, g1_flops, g1_bytes = algorithmic(geom, cfg.tokens, pairs, active, tok_local)
+    g2_flops, g2_bytes = gemm2_algorithmic(geom, pairs, active)
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = bytes_ / (ms * 1e-3) / 1e9
     t_floor_ms = max(flops / (PEAK_FP8_TFLOPS * 1e12), bytes_ / (PEAK_HBM_GBS * 1e9)) * 1e3
-    g1_ms = st["gemm1_swiglu"]
-    res = dict(workload=cfg.name, tokens=cfg.tokens, ms_per_call=ms, tflops=tflops, gb_s=gbs,
+    g1 = roofline_block("gemm1_swiglu", gemm1_kernel_name(cfg), st["gemm1_swiglu"], g1_flops,
+                        g1_bytes, PEAK_FP8_TFLOPS, cfg.name)
+    g2 = roofline_block("gemm2", gemm2_kernel_name(cfg), st["gemm2"], g2_flops, g2_bytes,
+                        PEAK_BF16_TFLOPS, cfg.name)
+    res = dict(workload=cfg.name, geometry=geom.name, tokens=cfg.tokens, seed=seed,
+               ms_per_call=ms, steps=steps, warmup_calls=n_warm, tflops=tflops, gb_s=gbs,
                pairs=pairs, active_experts=active, algorithmic_flops=flops,
-               algorithmic_bytes=bytes_, roofline_floor_ms=t_floor_ms,
-               roofline_frac=t_floor_ms / ms, hbm_frac=gbs / PEAK_HBM_GBS,
+               algorithmic_bytes=bytes_, call_floor_ms=t_floor_ms,
+               call_floor_frac=t_floor_ms / ms, hbm_frac=gbs / PEAK_HBM_GBS,
                fp8_mfma_frac=tflops / PEAK_FP8_TFLOPS, stage_ms=st,
-               gemm1=dict(ms=g1_ms, bytes=g1_bytes, flops=g1_flops,
-                          gb_s=g1_bytes / (g1_ms * 1e-3) / 1e9,
-                          tflops=g1_flops / (g1_ms * 1e-3) / 1e12))
+               roofline=g1 if st["gemm1_swiglu"] >= st["gemm2"] else g2,
+               kernels={"gemm1_swiglu": g1, "gemm2": g2})
     return res, kw
 
 
@@ -154,19 +199,29 @@ def measure_quant(T, H, steps, warmup, dev):
                 hbm_frac=gbs / PEAK_HBM_GBS)
 
 
+def _rows_hint(cfg):
+    g = cfg.geom
+    return cfg.tokens * g.top_k // g.num_experts
+
+
 def gemm1_kernel_name(cfg):
     """The GEMM1+SwiGLU kernel family the library picks for this shape: the shape-only rule of
     justgoal_amd/csrc/moe_gemm.hip (expected pairs per expert T*top_k/E: <= GEMM1_STREAM_MAX_ROWS
     streaming, >= GEMM1_BIG_ROWS large tiles, else LDS tiles)."""
-    g = cfg.geom
-    rows = cfg.tokens * g.top_k // g.num_experts
+    rows = _rows_hint(cfg)
     return ("gemm1_stream_kernel" if rows <= GEMM1_STREAM_MAX_ROWS else
             "gemm1_tile_kernel" if rows < GEMM1_BIG_ROWS else "gemm1_big_kernel")
 
 
-def load_traffic(name):
+def gemm2_kernel_name(cfg):
+    """GEMM2: streaming up to GEMM2_STREAM_MAX_ROWS expected pairs per expert, large tiles above."""
+    return ("gemm2_stream_kernel" if _rows_hint(cfg) <= GEMM2_STREAM_MAX_ROWS
+            else "gemm2_big_kernel")
+
+
+def load_traffic(stage, name):
     """HBM bytes per launch measured by rocprofv3 --pmc (committed under profiles/), if present."""
-    p = os.path.join(HERE, "profiles", f"traffic_gemm1_swiglu_{name}.json")
+    p = os.path.join(HERE, "profiles", f"traffic_{stage}_{name}.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -174,9 +229,10 @@ def load_traffic(name):
 
 
 def cpu_baseline(cfg, kw_dev, reps=3):
-    """The CPU oracle on this host's cores, on the full headline workload (median of ``reps``)."""
+    """The CPU oracle on all of this host's cores, on the full headline workload (median of
+    ``reps`` after one warm-up)."""
     import oracle
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = max(1, os.cpu_count() or 1)
     torch.set_num_threads(cores)
     kw = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in kw_dev.items()}
     geom = cfg.geom
@@ -188,18 +244,25 @@ def cpu_baseline(cfg, kw_dev, reps=3):
         ts.append(time.perf_counter() - t0)
     ts.sort()
     sec = ts[len(ts) // 2]
-    return sec, cores
+    return sec, torch.get_num_threads()
+
+
+DEFAULT_WORKLOADS = ("ds_t16", "ds_t64", "ds_t4096", "ds_t16384_skew", "qwen3_t1024")
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", default="ds_t64", choices=sorted(jin.CONFIGS))
-    ap.add_argument("--secondary", default="ds_t4096")
-    ap.add_argument("--sweep", action="store_true", help="also measure ds_t16384_skew and qwen3_t1024")
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="wall time of calls after the warm-up calls, before timing")
+    ap.add_argument("--config", default="ds_t64", choices=sorted(jin.CONFIGS),
+                    help="headline workload (value, ms_per_step)")
+    ap.add_argument("--workloads", default=",".join(DEFAULT_WORKLOADS),
+                    help="comma-separated workloads to measure (the headline is always included)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-quant", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device-to-device copies of 1 GiB (reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -220,65 +283,70 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    steps = max(20, args.steps)
     dev = torch.device("cuda:0")
     _lib.lib()
-    cfg = jin.CONFIGS[args.config]
-    t0 = time.time()
-    log(f"[bench] generating {cfg.geom.name} weights")
-    wts = tuple(t.to(dev) for t in jin.make_weights(cfg.geom, seed=0))
-    log(f"[bench] weights ready in {time.time() - t0:.1f}s; timing {cfg.name}")
-    head, head_kw = measure(cfg, wts, args.steps, args.warmup, dev)
-    log(f"[bench] {cfg.name}: {head['ms_per_call']:.4f} ms, {head['tflops']:.2f} TFLOPS, "
-        f"{head['gb_s']:.0f} GB/s, stages {head['stage_ms']}")
-    secondary = []
-    names = [args.secondary] if args.secondary else []
-    if args.sweep:
-        names += ["ds_t16384_skew", "qwen3_t1024"]
-    for n in names:
-        c = jin.CONFIGS[n]
-        if c.geom != cfg.geom:
-            log(f"[bench] generating {c.geom.name} weights")
-            w = tuple(t.to(dev) for t in jin.make_weights(c.geom, seed=0))
-        else:
-            w = wts
-        # The full warm-up count: clocks settle over tens of ms of load, whatever the call length.
-        r, _ = measure(c, w, max(5, args.steps // 4), args.warmup, dev)
-        log(f"[bench] {c.name}: {r['ms_per_call']:.4f} ms, {r['tflops']:.2f} TFLOPS, "
-            f"{r['gb_s']:.0f} GB/s, stages {r['stage_ms']}")
-        secondary.append(r)
-        del w
-    quant = [measure_quant(T, cfg.geom.hidden, args.steps, args.warmup, dev) for T in (4096, 64)]
+    head_cfg = jin.CONFIGS[args.config]
+    names = [n for n in args.workloads.split(",") if n]
+    if args.config not in names:
+        names.insert(0, args.config)
+    results, head, head_kw = {}, None, None
+    weights = {}
+    # group by geometry so each weight set is generated and resident once
+    for geom in dict.fromkeys(jin.CONFIGS[n].geom for n in names):
+        t0 = time.time()
+        log(f"[bench] generating {geom.name} weights")
+        wts = tuple(t.to(dev) for t in jin.make_weights(geom, seed=0))
+        log(f"[bench] weights ready in {time.time() - t0:.1f}s")
+        for n in names:
+            cfg = jin.CONFIGS[n]
+            if cfg.geom != geom:
+                continue
+            r, kw = measure(cfg, wts, steps, args.warmup, args.settle_ms, dev)
+            rl = r["roofline"]
+            log(f"[bench] {n}: {r['ms_per_call']:.4f} ms ({r['warmup_calls']} warm-up calls), "
+                f"{r['tflops']:.1f} TFLOPS, {r['gb_s']:.0f} GB/s, floor frac "
+                f"{r['call_floor_frac']:.3f}; {rl['kernel']} {rl['frac']:.3f} of {rl['bound']}; "
+                f"stages " + ", ".join(f"{k} {v * 1e3:.1f}us" for k, v in r["stage_ms"].items()))
+            results[n] = r
+            if n == args.config:
+                head, head_kw = r, kw
+            else:
+                del kw
+        del wts
+        torch.cuda.empty_cache()
+    quant = [] if args.no_quant else [
+        measure_quant(T, head_cfg.geom.hidden, steps, args.warmup, dev) for T in (4096, 64)]
     for r in quant:
         log(f"[bench] activation quant T={r['tokens']}: {r['ms_per_call'] * 1e3:.1f} us, "
             f"{r['gb_s']:.0f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU oracle")
-        sec, cores = cpu_baseline(cfg, head_kw)
+        sec, cores = cpu_baseline(head_cfg, head_kw)
         cpu = {"value": head["algorithmic_flops"] / sec / 1e12, "unit": "TFLOPS", "cores": cores,
                "kind": "port", "ms_per_call": sec * 1e3,
-               "sample": f"full {cfg.name} call (T={cfg.tokens}, {head['pairs']} local pairs), "
-                         "median of 3 after 1 warm-up, torch-CPU fp32 dequantise-then-matmul"}
-    g1 = head["gemm1"]
+               "sample": f"full {head_cfg.name} call (T={head_cfg.tokens}, {head['pairs']} local "
+                         "pairs), median of 3 after 1 warm-up, torch-CPU fp32 "
+                         "dequantise-then-matmul"}
     out = {
         "metric": METRIC, "value": head["tflops"], "unit": "TFLOPS", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms_per_call"],
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8-e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
-        "data": f"synthetic (seed {cfg.seed}: N(0,1) activations/logits, N(0,0.1) bias, "
+        "steps": steps, "warmup": args.warmup, "ms_per_step": head["ms_per_call"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
+        "data": f"synthetic (seed {head_cfg.seed}: N(0,1) activations/logits, N(0,0.1) bias, "
                 "N(0,0.02) weights, 128x128 block scales)",
-        "config": {"workload": cfg.name, "geometry": cfg.geom.name, "tokens": cfg.tokens,
-                   "seed": cfg.seed, "local_pairs": head["pairs"],
-                   "active_local_experts": head["active_experts"],
-                   "hidden": cfg.geom.hidden, "intermediate": cfg.geom.intermediate,
-                   "local_experts": cfg.geom.local_experts, "top_k": cfg.geom.top_k,
-                   "parallelism": "single GPU (EP rank 0 of 8: local experts 0..31)"},
-        "roofline": {"bound": "hbm", "kernel": gemm1_kernel_name(cfg), "achieved": g1["gb_s"],
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": g1["gb_s"] / PEAK_HBM_GBS,
-                     "traffic": load_traffic(cfg.name), "algorithmic_bytes": g1["bytes"],
-                     "avg_launch_ms": g1["ms"]},
+        "config": {"workload": head_cfg.name, "geometry": head_cfg.geom.name,
+                   "tokens": head_cfg.tokens, "seed": head_cfg.seed,
+                   "local_pairs": head["pairs"], "active_local_experts": head["active_experts"],
+                   "hidden": head_cfg.geom.hidden, "intermediate": head_cfg.geom.intermediate,
+                   "local_experts": head_cfg.geom.local_experts, "top_k": head_cfg.geom.top_k,
+                   "parallelism": "single GPU (EP rank 0 of 8: local experts 0..31)",
+                   "settle_ms": args.settle_ms},
+        "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "headline": head,
-        "secondary": secondary,
+        "workloads": {n: r for n, r in results.items() if n != args.config},
         "activation_quant": quant,
     }
     print(json.dumps(out), flush=True)

@@ -68,10 +68,12 @@ int moe_run(const void* logits, const void* bias, const void* hs, const void* hs
 
 /*
  * Workspace bytes moe_run needs for T tokens.
- * Replaces: `extern "C" int moe_workspace_bytes(int T)` (t1/kernel.cu:741). Returns int64: at
- * T=16384 the per-pair fp32 staging of this implementation exceeds INT_MAX bytes.
+ * Replaces: `extern "C" int moe_workspace_bytes(int T)` (t1/kernel.cu:741), same signature (the
+ * reference binds it with restype c_int, t1/main.py:64-65). DS-V3 needs about 133 KiB per
+ * token (bf16 C rows and bf16 partial rows): 1.88 GB at T = 14107. A size that does not fit in
+ * an int (T above 16107) returns MOE_ERR_INVALID_ARG; moe_workspace_bytes_ex gives it as int64.
  */
-int64_t moe_workspace_bytes(int T);
+int moe_workspace_bytes(int T);
 
 /* moe_run for any supported geometry (the reference hard-codes DS-V3; same arguments otherwise). */
 int moe_run_ex(const moe_geometry* geom, const void* logits, const void* bias, const void* hs,
@@ -101,9 +103,13 @@ enum {
   MOE_WS_SORTED_TOK,     /* int32 [Npmax]     token of each pair, ascending within an expert */
   MOE_WS_SORTED_W,       /* fp32  [Npmax]     routing weight of each pair */
   MOE_WS_C,              /* bf16  [Npmax, I]  SwiGLU activations */
-  MOE_WS_PARTIAL,        /* fp32  [Npmax, H]  weighted GEMM2 rows */
+  MOE_WS_PARTIAL,        /* bf16  [T * (k - 1), H]  weighted GEMM2 rows of each token's 2nd..k-th
+                            local pair (k = min(top_k, E_l)); the 1st goes straight into `out` */
   MOE_WS_CHUNK_COUNTS,   /* int32 [ceil(T/c), E_l] pairs per local expert per c-token group,
                             c = 4 for T <= 256, else 16 (one row per routing workgroup) */
+  MOE_WS_PAIR_DST,       /* int32 [Npmax]     GEMM2 destination of each pair: t (row of out) for
+                            a token's first local pair, else -1 - (t * (k - 1) + j - 1) for its
+                            (j+1)-th (row of partial) */
   MOE_WS_NUM_REGIONS     /* total size is written at this index */
 };
 

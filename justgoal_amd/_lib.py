@@ -18,9 +18,9 @@ EXPORTED = ("moe_run", "moe_workspace_bytes", "moe_run_ex", "moe_workspace_bytes
             "moe_route_ex", "moe_workspace_layout", "moe_set_stage_events", "moe_error_string",
             "moe_quantize_activations")
 
-MOE_WS_NUM_REGIONS = 10
+MOE_WS_NUM_REGIONS = 11
 WS_REGIONS = ("topk_idx", "topk_w", "pair_of", "counts", "offsets", "sorted_tok", "sorted_w", "C",
-              "partial", "chunk_counts")
+              "partial", "chunk_counts", "pair_dst")
 
 _LIB = None
 
@@ -40,7 +40,7 @@ def lib() -> ctypes.CDLL:
         L.moe_run.argtypes = [P] * 8 + [I, F, P, P, I, P]
         L.moe_run.restype = I
         L.moe_workspace_bytes.argtypes = [I]
-        L.moe_workspace_bytes.restype = ctypes.c_int64
+        L.moe_workspace_bytes.restype = I
         L.moe_run_ex.argtypes = [G] + [P] * 8 + [I, F, P, P, I, P]
         L.moe_run_ex.restype = I
         L.moe_workspace_bytes_ex.argtypes = [G, I]

@@ -44,10 +44,12 @@ int check_geometry(const moe_geometry* g) {
   return MOE_OK;
 }
 
-int64_t max_pairs(const moe_geometry* g, int T) {
-  const int k = g->top_k < g->local_experts ? g->top_k : g->local_experts;
-  return (int64_t)T * k;
+// Local pairs a token can have: min(top_k, E_l).
+int k_local(const moe_geometry* g) {
+  return g->top_k < g->local_experts ? g->top_k : g->local_experts;
 }
+
+int64_t max_pairs(const moe_geometry* g, int T) { return (int64_t)T * k_local(g); }
 
 // Most tokens one moe_run call takes. The kernels address activations, C rows and their scales
 // with 32-bit buffer offsets: T*H must stay below the large-tile kernels' out-of-range marker
@@ -70,8 +72,9 @@ void layout(const moe_geometry* g, int T, int64_t* off) {
       4 * Np,                            // sorted_tok
       4 * Np,                            // sorted_w
       2 * Np * g->intermediate,          // C (bf16)
-      4 * Np * g->hidden,                // partial (fp32)
+      2 * (int64_t)T * (k_local(g) - 1) * g->hidden,  // partial (bf16, pairs 2.. of a token)
       4 * (int64_t)jgmoe::route_chunks(T) * El,  // chunk count rows
+      4 * Np,                            // pair_dst
   };
   int64_t cur = 0;
   for (int i = 0; i < MOE_WS_NUM_REGIONS; ++i) {
@@ -109,8 +112,9 @@ struct Regions {
   int32_t* sorted_tok;
   float* sorted_w;
   uint16_t* C;
-  float* partial;
+  uint16_t* partial;
   int32_t* hist;
+  int32_t* pair_dst;
 };
 
 Regions carve(const moe_geometry* g, int T, void* ws) {
@@ -121,7 +125,8 @@ Regions carve(const moe_geometry* g, int T, void* ws) {
                  (int32_t*)(b + off[MOE_WS_PAIR_OF]),  (int32_t*)(b + off[MOE_WS_COUNTS]),
                  (int32_t*)(b + off[MOE_WS_OFFSETS]),  (int32_t*)(b + off[MOE_WS_SORTED_TOK]),
                  (float*)(b + off[MOE_WS_SORTED_W]),   (uint16_t*)(b + off[MOE_WS_C]),
-                 (float*)(b + off[MOE_WS_PARTIAL]), (int32_t*)(b + off[MOE_WS_CHUNK_COUNTS])};
+                 (uint16_t*)(b + off[MOE_WS_PARTIAL]), (int32_t*)(b + off[MOE_WS_CHUNK_COUNTS]),
+                 (int32_t*)(b + off[MOE_WS_PAIR_DST])};
 }
 
 #define JG_TRY(expr)                              \
@@ -143,7 +148,7 @@ int route_and_permute(const moe_geometry* g, const void* logits, const void* bia
   JG_TRY(mark_stage(1, stream));
   JG_TRY(jgmoe::launch_permute(r.topk_idx, r.topk_w, r.hist, T, g->top_k, local_offset,
                                g->local_experts, r.counts, r.offsets, r.sorted_tok, r.sorted_w,
-                               r.pair_of, stream));
+                               r.pair_dst, r.pair_of, stream));
   JG_TRY(mark_stage(2, stream));
   return MOE_OK;
 }
@@ -182,7 +187,10 @@ int64_t moe_workspace_bytes_ex(const moe_geometry* geom, int T) {
   return off[MOE_WS_NUM_REGIONS];
 }
 
-int64_t moe_workspace_bytes(int T) { return moe_workspace_bytes_ex(&kDsV3, T); }
+int moe_workspace_bytes(int T) {
+  const int64_t n = moe_workspace_bytes_ex(&kDsV3, T);
+  return n > INT32_MAX ? MOE_ERR_INVALID_ARG : (int)n;
+}
 
 int moe_workspace_layout(const moe_geometry* geom, int T, int64_t* offsets) {
   const int rc = check_geometry(geom);
@@ -227,9 +235,11 @@ int moe_run_ex(const moe_geometry* geom, const void* logits, const void* bias, c
                              El, Np, rows_hint, stream));
   JG_TRY(mark_stage(3, stream));
   JG_TRY(jgmoe::launch_gemm2(r.C, (const uint8_t*)w2, (const float*)s2, r.counts, r.offsets,
-                             r.sorted_w, r.partial, H, I, El, Np, rows_hint, stream));
+                             r.sorted_w, jgmoe::Gemm2Out{r.pair_dst, (uint16_t*)out, r.partial},
+                             H, I, El, Np, rows_hint, stream));
   JG_TRY(mark_stage(4, stream));
-  JG_TRY(jgmoe::launch_combine(r.partial, r.pair_of, T, geom->top_k, H, (uint16_t*)out, stream));
+  JG_TRY(jgmoe::launch_combine(r.partial, r.pair_of, T, geom->top_k, k_local(geom), H,
+                               (uint16_t*)out, stream));
   JG_TRY(mark_stage(5, stream));
   return MOE_OK;
 }

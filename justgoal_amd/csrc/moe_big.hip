@@ -10,7 +10,8 @@
 //   activation scales, and 128 columns of C, i.e. 128 X1 rows and 128 X2 rows of W13. The
 //   epilogue applies SwiGLU and stores bf16 C.
 // * GEMM2: 128 rows of bf16 C and 128 rows of W2; the epilogue scales by the pair's routing
-//   weight and stores fp32 rows for the combine.
+//   weight and stores bf16 rows at the pair's destination (the token's output row for its first
+//   local pair, else one of its partial rows for the combine).
 //
 // Per K step the producer waits for its own DMAs of the step's block (counted vmcnt), passes the
 // workgroup barrier and refills the slot freed by the previous step with the block two steps
@@ -23,12 +24,6 @@
 
 #ifndef JG_XCD_MAP
 #define JG_XCD_MAP 0
-#endif
-#ifndef JG_ABL_NODMA
-#define JG_ABL_NODMA 0
-#endif
-#ifndef JG_ABL_NOMMA
-#define JG_ABL_NOMMA 0
 #endif
 
 namespace jgmoe {
@@ -194,7 +189,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
     };
 #pragma unroll
     for (int d = 0; d < D - 1; ++d) {
-      if (!JG_ABL_NODMA) issue(cur, d, d);
+      issue(cur, d, d);
       __builtin_amdgcn_sched_barrier(0);
     }
     int slot = 0;
@@ -208,14 +203,14 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
       for (; kb + D - 1 < NKB; ++kb) {
         vm_wait<vm_depth((D - 2) * OPS)>();  // the DMAs of block kb have landed
         __builtin_amdgcn_s_barrier();
-        if (!JG_ABL_NODMA) issue(cur, kb + D - 1, slot == 0 ? D - 1 : slot - 1);
+        issue(cur, kb + D - 1, slot == 0 ? D - 1 : slot - 1);
         __builtin_amdgcn_sched_barrier(0);
         slot = slot + 1 == D ? 0 : slot + 1;
       }
       for (; kb < NKB; ++kb) {
         vm_wait<vm_depth((D - 2) * OPS)>();
         __builtin_amdgcn_s_barrier();
-        if (!JG_ABL_NODMA) issue(nxt, kb + D - 1 - NKB, slot == 0 ? D - 1 : slot - 1);
+        issue(nxt, kb + D - 1 - NKB, slot == 0 ? D - 1 : slot - 1);
         __builtin_amdgcn_sched_barrier(0);
         slot = slot + 1 == D ? 0 : slot + 1;
       }
@@ -439,8 +434,7 @@ template <int MS, int NS, int D, int WM, int WN>
 __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const float* __restrict__ sorted_w, float* __restrict__ partial, int H, int I, int E_l,
-    int max_pairs) {
+    const float* __restrict__ sorted_w, Gemm2Out dst, int H, int I, int E_l, int max_pairs) {
   static_assert(D >= 3, "the prefetch lead is D-1 blocks");
   static_assert(16 * NS <= kBlock && kBlock % (16 * NS) == 0, "a wave's columns share one scale block");
   constexpr int BM = 16 * MS * WM, BN = 16 * NS * WN;
@@ -449,7 +443,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
   constexpr int AI = BM / 4;          // C DMA instructions per step (4 rows x 256 B each)
   constexpr int BI = BN / 8;          // W2 DMA instructions per step (8 rows x 128 B each)
   constexpr int OPS = AI + BI;
-  constexpr int MW = MS + 2;          // compute-wave metadata dwords per lane
+  constexpr int MW = 2 * MS + 2;      // compute-wave metadata dwords per lane
   constexpr int ASZ = BM * ARow, BSZ = BN * kBlock;
   __shared__ __attribute__((aligned(16))) uint8_t aring[D][ASZ];
   __shared__ __attribute__((aligned(16))) uint8_t bring[D][BSZ];
@@ -509,7 +503,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     };
 #pragma unroll
     for (int d = 0; d < D - 1; ++d) {
-      if (!JG_ABL_NODMA) issue(false, d, d);
+      issue(false, d, d);
       __builtin_amdgcn_sched_barrier(0);
     }
     int slot = 0;
@@ -522,7 +516,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
         __builtin_amdgcn_s_barrier();
         const int kn = kb + D - 1;
         const bool second = kn >= NKB;
-        if (!JG_ABL_NODMA) issue(second, second ? kn - NKB : kn, slot == 0 ? D - 1 : slot - 1);
+        issue(second, second ? kn - NKB : kn, slot == 0 ? D - 1 : slot - 1);
         __builtin_amdgcn_sched_barrier(0);
         slot = slot + 1 == D ? 0 : slot + 1;
         ++kb;
@@ -544,6 +538,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
   const int wm = w / WN, wn = w % WN;
   const int r16 = lane & 15, g = lane >> 4;
   const __amdgpu_buffer_rsrc_t wgtres = make_rsrc(sorted_w, (uint32_t)max_pairs * 4);
+  const __amdgpu_buffer_rsrc_t dstres = make_rsrc(dst.pair_dst, (uint32_t)max_pairs * 4);
   const __amdgpu_buffer_rsrc_t s2res = make_rsrc(s2, (uint32_t)E_l * (H / kBlock) * NKB * 4);
   const uint32_t rd0 = wblk_read_off(lane, 0), rd1 = wblk_read_off(lane, 1);
   float* my_meta = &mring[w][0][0];
@@ -551,6 +546,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     B2Scalars s;
     LaneScales sc;  // weight scales of this wave's columns (one 128-block)
     float wgt[MS];  // routing weight of the lane's output row in each sub-tile
+    int dst[MS];    // destination row code (pair_dst) of that row
   };
   auto meta = [&](int item, Q& x) {
     scalars(item, x.s);
@@ -559,6 +555,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     for (int ms = 0; ms < MS; ++ms) {
       const int r = x.s.m0 + (wm * MS + ms) * 16 + r16;
       dma4(wgtres, my_meta + ms * kWave, 4u * (x.s.seg + (r < last ? r : last)), 0);
+      dma4(dstres, my_meta + (MS + 2 + ms) * kWave, 4u * (x.s.seg + (r < last ? r : last)), 0);
     }
     const int wc = x.s.h0 + wn * 16 * NS;
     const uint32_t so =
@@ -575,7 +572,10 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
 #pragma unroll
     for (int j = 0; j < MW; ++j) lds_fence(v[j]);
 #pragma unroll
-    for (int ms = 0; ms < MS; ++ms) x.wgt[ms] = v[ms];
+    for (int ms = 0; ms < MS; ++ms) {
+      x.wgt[ms] = v[ms];
+      x.dst[ms] = __float_as_int(v[MS + 2 + ms]);
+    }
     x.sc.v0 = v[MS];
     x.sc.v1 = v[MS + 1];
   };
@@ -718,11 +718,17 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
       const int r = cur.s.m0 + (wm * MS + ms) * 16 + r16;
       if (r < cur.s.cnt) {
         const float wp = cur.wgt[ms];
-        float* orow = partial + (size_t)(cur.s.seg + r) * H + cur.s.h0 + wn * 16 * NS + 4 * g;
+        const int d = cur.dst[ms];
+        uint16_t* orow = (d >= 0 ? dst.out + (size_t)d * H : dst.partial + (size_t)(-1 - d) * H) +
+                         cur.s.h0 + wn * 16 * NS + 4 * g;
 #pragma unroll
-        for (int ns = 0; ns < NS; ++ns)
-          *(float4*)(orow + 16 * ns) = float4{acc[ms][ns][0] * wp, acc[ms][ns][1] * wp,
-                                              acc[ms][ns][2] * wp, acc[ms][ns][3] * wp};
+        for (int ns = 0; ns < NS; ++ns) {
+          const uint32_t h01 = (uint32_t)float_to_bf16_bits(acc[ms][ns][0] * wp) |
+                               ((uint32_t)float_to_bf16_bits(acc[ms][ns][1] * wp) << 16);
+          const uint32_t h23 = (uint32_t)float_to_bf16_bits(acc[ms][ns][2] * wp) |
+                               ((uint32_t)float_to_bf16_bits(acc[ms][ns][3] * wp) << 16);
+          *(uint2*)(orow + 16 * ns) = uint2{h01, h23};
+        }
       }
     }
     if (it_n >= items) break;
@@ -792,13 +798,13 @@ hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint
 
 hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s2,
                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
-                            float* partial, int H, int I, int E_l, int max_pairs,
+                            Gemm2Out dst, int H, int I, int E_l, int max_pairs,
                             hipStream_t stream) {
   constexpr int BN = 16 * JG_B2_NS * JG_B2_WN;
   if (H % BN != 0 || I / kBlock < JG_B2_D - 1) return hipErrorNotSupported;
   const int grid = big_grid(big_tiles(max_pairs, 16 * JG_B2_MS * JG_B2_WM, E_l) * (H / BN));
   gemm2_big_kernel<JG_B2_MS, JG_B2_NS, JG_B2_D, JG_B2_WM, JG_B2_WN><<<grid, (JG_B2_WM * JG_B2_WN + 1) * kWave, 0, stream>>>(
-      C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs);
+      C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs);
   return hipGetLastError();
 }
 

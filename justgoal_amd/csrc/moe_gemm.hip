@@ -8,7 +8,8 @@
 // (not requantised to fp8 as the reference solutions do at main.py:151-156); GEMM2 converts the
 // W2 e4m3 bytes to bf16 exactly, runs four v_mfma_f32_16x16x32_bf16 per K block (lane group
 // g = lane>>4 carries K = 32g + 8c .. +8 for instruction c, the same map on both operands), scales
-// by s2[e, h/128, kb] and writes fp32 rows times the pair's routing weight.
+// by s2[e, h/128, kb] and stores bf16 rows times the pair's routing weight at the pair's
+// destination row (out for a token's first local pair, else a partial row for combine_kernel).
 //
 // The choice of kernel family depends only on shapes (never on routed counts, which stay on the
 // device): see launch_gemm1 / launch_gemm2 below.
@@ -19,49 +20,48 @@
 
 namespace jgmoe {
 
-// Workgroup = (token, 1024 consecutive hidden columns), 8 columns per thread. Each wave reads
-// the token's K pair indices once (one lane each), orders them ascending in scalar registers
-// (pair rows ascend with the local expert, the oracle's summation order) and streams the rows.
+// Workgroup = (token, 1024 consecutive hidden columns), 8 columns per thread. The token's local
+// pair count n comes from its pair_of row (one lane per slot, reduced by a ballot). GEMM2 has
+// already stored the first pair's weighted row in out[t] and pairs 2..n in the token's partial
+// rows (contiguous, ascending local expert), all bf16; the sum runs in fp32 in that order.
 constexpr int kCombineThreads = 128;
 
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
-    const float* __restrict__ partial, const int32_t* __restrict__ pair_of, int T, int K, int H,
-    uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ partial, const int32_t* __restrict__ pair_of, int T, int K,
+    int k_local, int H, uint16_t* __restrict__ out) {
   const int H8 = H / 8;
   const int chunks = (H8 + kCombineThreads - 1) / kCombineThreads;
   const int t = blockIdx.x / chunks;
   const int c8 = (blockIdx.x % chunks) * kCombineThreads + threadIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
-  const int q = lane < K ? pair_of[(size_t)t * K + lane] : -1;
-  int p[kMaxTopK];
-  int n = 0;
-#pragma unroll
-  for (int k = 0; k < kMaxTopK; ++k) {
-    const int v = __builtin_amdgcn_readlane(q, k);
-    if (k < K && v >= 0) {
-      int j = n++;
-      while (j > 0 && p[j - 1] > v) {
-        p[j] = p[j - 1];
-        --j;
-      }
-      p[j] = v;
-    }
-  }
-  if (c8 >= H8) return;
+  const bool local = lane < K && pair_of[(size_t)t * K + lane] >= 0;
+  const int n = __popcll(__ballot(local));
+  if (n == 1 || c8 >= H8) return;  // one local pair: GEMM2 wrote the final row
   const int c = c8 * 8;
-  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < n; ++j) {
-    const float4* src = (const float4*)(partial + (size_t)p[j] * H + c);
-    const float4 u = src[0], v = src[1];
-    s[0] += u.x; s[1] += u.y; s[2] += u.z; s[3] += u.w;
-    s[4] += v.x; s[5] += v.y; s[6] += v.z; s[7] += v.w;
+  uint4* dst = (uint4*)(out + (size_t)t * H + c);
+  if (n == 0) {
+    *dst = uint4{0u, 0u, 0u, 0u};
+    return;
   }
+  float s[8];
+  auto add = [&](uint4 v, bool first) {
+    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = __uint_as_float(u[i] << 16), hi = __uint_as_float(u[i] & 0xffff0000u);
+      s[2 * i] = first ? lo : s[2 * i] + lo;
+      s[2 * i + 1] = first ? hi : s[2 * i + 1] + hi;
+    }
+  };
+  add(*dst, true);
+  const uint16_t* prow = partial + (size_t)t * (k_local - 1) * H + c;
+  for (int j = 0; j + 1 < n; ++j) add(*(const uint4*)(prow + (size_t)j * H), false);
   uint4 o;
   o.x = (uint32_t)float_to_bf16_bits(s[0]) | ((uint32_t)float_to_bf16_bits(s[1]) << 16);
   o.y = (uint32_t)float_to_bf16_bits(s[2]) | ((uint32_t)float_to_bf16_bits(s[3]) << 16);
   o.z = (uint32_t)float_to_bf16_bits(s[4]) | ((uint32_t)float_to_bf16_bits(s[5]) << 16);
   o.w = (uint32_t)float_to_bf16_bits(s[6]) | ((uint32_t)float_to_bf16_bits(s[7]) << 16);
-  *(uint4*)(out + (size_t)t * H + c) = o;
+  *dst = o;
 }
 
 // Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from a sweep
@@ -121,18 +121,18 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t*
 
 hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
                         const int32_t* counts, const int32_t* offsets, const float* sorted_w,
-                        float* partial, int H, int I, int E_l, int max_pairs, int rows_hint,
+                        Gemm2Out dst, int H, int I, int E_l, int max_pairs, int rows_hint,
                         hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
   if (rows_hint <= JG_G2_STREAM_MAX_ROWS)
-    return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
+    return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
                                max_pairs, stream_mt(rows_hint), stream);
   if (rows_hint >= JG_G2_BIG_ROWS) {
-    const hipError_t b = launch_gemm2_big(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l,
+    const hipError_t b = launch_gemm2_big(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
                                           max_pairs, stream);
     if (b != hipErrorNotSupported) return b;
   }
-  return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs,
+  return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs,
                              4, stream);
 }
 
@@ -152,12 +152,12 @@ int device_cu_count() {
   return cus[dev];
 }
 
-hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,
-                          uint16_t* out, hipStream_t stream) {
+hipError_t launch_combine(const uint16_t* partial, const int32_t* pair_of, int T, int K,
+                          int k_local, int H, uint16_t* out, hipStream_t stream) {
   if (T == 0) return hipSuccess;
   const long long chunks = (H / 8 + kCombineThreads - 1) / kCombineThreads;
-  combine_kernel<<<dim3((unsigned)(T * chunks)), kCombineThreads, 0, stream>>>(partial, pair_of, T,
-                                                                               K, H, out);
+  combine_kernel<<<dim3((unsigned)(T * chunks)), kCombineThreads, 0, stream>>>(
+      partial, pair_of, T, K, k_local, H, out);
   return hipGetLastError();
 }
 

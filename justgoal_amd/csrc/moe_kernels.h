@@ -15,11 +15,12 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, int T, int E,
                         int E_l, int32_t* topk_idx, float* topk_w, int32_t* hist,
                         hipStream_t stream);
 
-// Segment layout (counts, offsets, sorted tokens/weights, pair map) from the count rows.
+// Segment layout (counts, offsets, sorted tokens/weights, pair map) from the count rows, and
+// each pair's GEMM2 destination row (pair_dst, encoded as described at launch_gemm2).
 hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, const int32_t* hist,
                           int T, int K, int local_offset, int E_l, int32_t* counts,
                           int32_t* offsets, int32_t* sorted_tok, float* sorted_w,
-                          int32_t* pair_of, hipStream_t stream);
+                          int32_t* pair_dst, int32_t* pair_of, hipStream_t stream);
 
 // Number of routing workgroups (4 tokens each up to T = 256, 16 above) = rows of the chunk count
 // table.
@@ -33,10 +34,18 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t*
                         const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                         int max_pairs, int rows_hint, hipStream_t stream);
 
-// Grouped GEMM2 (W2): partial[p, :] = w_p * (C[p, :] @ W2[e]^T) in fp32.
+// Grouped GEMM2 (W2): row = bf16(w_p * (C[p, :] @ W2[e]^T)), stored at the pair's destination
+// d = pair_dst[p]: out row d when d >= 0 (the token's first local pair in ascending expert
+// order), else partial row -1 - d (its later pairs; bf16 [T * (min(top_k, E_l) - 1), H]).
+struct Gemm2Out {
+  const int32_t* pair_dst;
+  uint16_t* out;
+  uint16_t* partial;
+};
 hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
                         const int32_t* counts, const int32_t* offsets, const float* sorted_w,
-                        float* partial, int H, int I, int E_l, int max_pairs, int rows_hint, hipStream_t stream);
+                        Gemm2Out dst, int H, int I, int E_l, int max_pairs, int rows_hint,
+                        hipStream_t stream);
 
 // Persistent weight-streaming variants for segments of at most a few 16-row tiles.
 hipError_t launch_gemm1_stream(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
@@ -45,7 +54,7 @@ hipError_t launch_gemm1_stream(const uint8_t* hs, const float* hs_scale, const u
                                int E_l, int max_pairs, int mt, hipStream_t stream);
 hipError_t launch_gemm2_stream(const uint16_t* C, const uint8_t* w2, const float* s2,
                                const int32_t* counts, const int32_t* offsets,
-                               const float* sorted_w, float* partial, int H, int I, int E_l,
+                               const float* sorted_w, Gemm2Out dst, int H, int I, int E_l,
                                int max_pairs, int mt, hipStream_t stream);
 
 // Large-tile variants (BM x BN per workgroup, both operands shared through LDS) for long
@@ -56,7 +65,7 @@ hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint
                             int max_pairs, hipStream_t stream);
 hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s2,
                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
-                            float* partial, int H, int I, int E_l, int max_pairs,
+                            Gemm2Out dst, int H, int I, int E_l, int max_pairs,
                             hipStream_t stream);
 
 // LDS-tiled variants for longer segments (mt = 16-row sub-tiles per workgroup tile).
@@ -64,13 +73,15 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
                              const float* s13, const int32_t* counts, const int32_t* offsets,
                              const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                              int max_pairs, int mt, hipStream_t stream);
-// out[t, :] = bf16(sum of partial rows of t's local pairs, ascending local expert), 0 if none.
 // Compute units of the current device, queried once per device (thread-safe); 256 when the
 // query fails. Sizes the persistent grids.
 int device_cu_count();
 
-hipError_t launch_combine(const float* partial, const int32_t* pair_of, int T, int K, int H,
-                          uint16_t* out, hipStream_t stream);
+// Finishes the output after GEMM2: a token with no local pair gets a zero row; one with n >= 2
+// gets bf16(out[t] + partial rows 0..n-2 of t, summed in fp32 in that order, i.e. ascending
+// local expert); a token with exactly one local pair keeps the row GEMM2 wrote.
+hipError_t launch_combine(const uint16_t* partial, const int32_t* pair_of, int T, int K,
+                          int k_local, int H, uint16_t* out, hipStream_t stream);
 
 // Activation quantisation: bf16 [T, H] -> e4m3 [T, H] and fp32 scales [H/128, T] (1x128 blocks,
 // scale = amax / 448). H must be a multiple of 128.

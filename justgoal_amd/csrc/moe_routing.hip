@@ -231,8 +231,10 @@ __device__ __forceinline__ void build_masks(const TokenPairs& tp, int n, int top
 // number of earlier rows that also selected e, so each segment stays in ascending token order.
 __device__ __forceinline__ void place_from_masks(const TokenPairs& tp, const ExpertMasks& m,
                                                  int n, int t0, int T, int top_k,
-                                                 const int* base, int32_t* __restrict__ sorted_tok,
+                                                 const int* base, int k_local,
+                                                 int32_t* __restrict__ sorted_tok,
                                                  float* __restrict__ sorted_w,
+                                                 int32_t* __restrict__ pair_dst,
                                                  int32_t* __restrict__ pair_of) {
   for (int i = threadIdx.x; i < n * top_k; i += blockDim.x) {
     const int r = i / top_k, k = i % top_k, t = t0 + r;
@@ -241,8 +243,17 @@ __device__ __forceinline__ void place_from_masks(const TokenPairs& tp, const Exp
       int rank = __popcll(m.bits[e][r >> 6] & ((1ull << (r & 63)) - 1ull));
       for (int w = 0; w < (r >> 6); ++w) rank += __popcll(m.bits[e][w]);
       const int p = base[e] + rank;
+      // Rank of this pair among the token's local pairs in ascending local-expert order: the
+      // first goes straight into the output row, the others into the token's partial rows.
+      int j = 0;
+#pragma unroll
+      for (int q = 0; q < kMaxTopK; ++q) {
+        const int o = tp.le[r][q];
+        j += (o >= 0 && o < e);
+      }
       sorted_tok[p] = t;
       sorted_w[p] = tp.w[r][k];
+      pair_dst[p] = j == 0 ? t : -(1 + t * (k_local - 1) + (j - 1));
       pair_of[(size_t)t * top_k + k] = p;
     } else if (t < T) {
       pair_of[(size_t)t * top_k + k] = -1;
@@ -323,7 +334,7 @@ __global__ __launch_bounds__(256) void permute_kernel(
     const int32_t* __restrict__ hist, int T, int K, int local_offset, int E_l, int n_rows,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_tok, float* __restrict__ sorted_w,
-    int32_t* __restrict__ pair_of) {
+    int32_t* __restrict__ pair_dst, int32_t* __restrict__ pair_of) {
   __shared__ TokenPairs tp;  // rows 0..63 used
   __shared__ ExpertMasks masks;
   __shared__ int chunk_cnt[kMaxLocal];
@@ -382,7 +393,8 @@ __global__ __launch_bounds__(256) void permute_kernel(
     }
   if (threadIdx.x < E_l) before[threadIdx.x] += off[threadIdx.x];
   __syncthreads();
-  place_from_masks(tp, masks, n, t0, T, K, before, sorted_tok, sorted_w, pair_of);
+  place_from_masks(tp, masks, n, t0, T, K, before, min(K, E_l), sorted_tok, sorted_w, pair_dst,
+                   pair_of);
 }
 
 int route_chunks(int T) {
@@ -419,12 +431,12 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, int T, int E,
 hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, const int32_t* hist,
                           int T, int K, int local_offset, int E_l, int32_t* counts,
                           int32_t* offsets, int32_t* sorted_tok, float* sorted_w,
-                          int32_t* pair_of, hipStream_t stream) {
+                          int32_t* pair_dst, int32_t* pair_of, hipStream_t stream) {
   const int blocks = (T + kPlaceTokens - 1) / kPlaceTokens;
   permute_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(topk_idx, topk_w, hist, T, K,
                                                         local_offset, E_l, route_chunks(T),
                                                         counts, offsets, sorted_tok, sorted_w,
-                                                        pair_of);
+                                                        pair_dst, pair_of);
   return hipGetLastError();
 }
 

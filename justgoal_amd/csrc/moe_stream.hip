@@ -23,16 +23,11 @@
 // (pair) l & 15. GEMM1 applies the activation scale (one per lane) times the weight scale of the
 // K block after every fp8 MFMA and ends with SwiGLU into bf16 C; GEMM2 converts the fp8 weight
 // block to bf16 in registers, runs four bf16 MFMAs per K block over the bf16 C rows, scales by
-// the block's weight scale, and writes fp32 rows times the pair's routing weight.
+// the block's weight scale, and stores bf16 rows times the pair's routing weight at the pair's
+// destination (the output row for a token's first local pair, else one of its partial rows).
 #include "moe_device.h"
 #include "moe_kernels.h"
 
-#ifndef JG_G2S_BOUNDED
-#define JG_G2S_BOUNDED 0
-#endif
-#ifndef JG_ABL_NOC
-#define JG_ABL_NOC 0
-#endif
 
 namespace jgmoe {
 
@@ -243,7 +238,7 @@ __global__ __launch_bounds__(256) void gemm1_stream_kernel(
   vm_wait<0>();  // no DMA may still target this workgroup's LDS when it retires
 }
 
-// ---- GEMM2: partial = (C W2^T) * routing weight -----------------------------------------------
+// ---- GEMM2: bf16((C W2^T) * routing weight) into the pair's destination row ---------------------
 
 template <int MT>
 struct G2Slot {
@@ -257,8 +252,7 @@ struct G2Item {
   LaneScales sc;         // weight scales of the 128-row block holding h0, per K block
   uint32_t coff[MT];     // per lane: byte offset of C[pair][32 g]
   float wgt[MT];         // routing weight of the lane's pair
-  const uint16_t* cbase; // C row of the tile's first pair
-  uint32_t crec;         // bytes of C from cbase to the segment's end
+  int dst[MT];           // destination row code of the lane's pair (pair_dst)
   int m0, cnt, seg, h0;
 };
 
@@ -266,8 +260,7 @@ template <int MT, int D>
 __global__ __launch_bounds__(256) void gemm2_stream_kernel(
     const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const float* __restrict__ sorted_w, float* __restrict__ partial, int H, int I, int E_l,
-    int max_pairs) {
+    const float* __restrict__ sorted_w, Gemm2Out dst, int H, int I, int E_l, int max_pairs) {
   constexpr int BM = 16 * MT;
   constexpr int OPS = 4 * MT + 2;
   __shared__ __attribute__((aligned(16))) uint8_t ring[kWavesPerGroup][D][kWBlk];
@@ -302,12 +295,10 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
     for (int mt = 0; mt < MT; ++mt) {
       const int r = x.m0 + mt * 16 + r16;
       const int p = x.seg + (r < x.cnt ? r : x.cnt - 1);
-      x.coff[mt] = JG_G2S_BOUNDED ? ((uint32_t)(mt * 16 + r16) * I + 32 * g) * 2
-                                  : ((uint32_t)p * I + 32 * g) * 2;
+      x.coff[mt] = ((uint32_t)p * I + 32 * g) * 2;
       x.wgt[mt] = sorted_w[p];
+      x.dst[mt] = dst.pair_dst[p];
     }
-    x.cbase = uniform(C + (size_t)(x.seg + x.m0) * I);
-    x.crec = uniform((uint32_t)(x.cnt - x.m0) * I * 2);
   };
 
   G2Item<MT> cur, nxt, nn;
@@ -319,16 +310,13 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
   // As in GEMM1, prefetches past a wave's last item use an out-of-range offset (no traffic).
   auto issue = [&](bool second, int kbi, G2Slot<MT>& s, int d) {
     const bool dead = uniform(second && it_n >= items);
-    const __amdgpu_buffer_rsrc_t cr =
-        JG_G2S_BOUNDED ? make_rsrc(uniform(second ? nxt.cbase : cur.cbase),
-                                   uniform(second ? nxt.crec : cur.crec))
-                       : cres;
+    const __amdgpu_buffer_rsrc_t cr = cres;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const uint32_t co = dead ? kNoFetch : second ? nxt.coff[mt] : cur.coff[mt];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        s.a[mt][c] = JG_ABL_NOC ? uint4{0, 0, 0, 0} : buf_load16(cr, co, 2 * (kbi * kBlock + 8 * c));
+        s.a[mt][c] = buf_load16(cr, co, 2 * (kbi * kBlock + 8 * c));
     }
     const __amdgpu_buffer_rsrc_t wres =
         make_rsrc(uniform(second ? nxt.wbase : cur.wbase), (uint32_t)H * I);
@@ -348,7 +336,10 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
   retire(nxt.sc.v0);  // loop entry must not carry pending loads (see the K loop)
   retire(nxt.sc.v1);
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) retire(nxt.wgt[mt]);
+  for (int mt = 0; mt < MT; ++mt) {
+    retire(nxt.wgt[mt]);
+    retire(nxt.dst[mt]);
+  }
 
   for (;;) {
     const int it_nn = it_n + stride;
@@ -393,7 +384,10 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
       retire(nn.sc.v0);
       retire(nn.sc.v1);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) retire(nn.wgt[mt]);
+      for (int mt = 0; mt < MT; ++mt) {
+        retire(nn.wgt[mt]);
+        retire(nn.dst[mt]);
+      }
       kb0 += D;
     } while (kb0 < NKB);
 
@@ -402,8 +396,13 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
       const int r = cur.m0 + mt * 16 + r16;
       if (r < cur.cnt) {
         const float wp = cur.wgt[mt];
-        *(float4*)(partial + (size_t)(cur.seg + r) * H + cur.h0 + 4 * g) =
-            float4{acc[mt][0] * wp, acc[mt][1] * wp, acc[mt][2] * wp, acc[mt][3] * wp};
+        const int d = cur.dst[mt];
+        uint16_t* row = d >= 0 ? dst.out + (size_t)d * H : dst.partial + (size_t)(-1 - d) * H;
+        const uint32_t h01 = (uint32_t)float_to_bf16_bits(acc[mt][0] * wp) |
+                             ((uint32_t)float_to_bf16_bits(acc[mt][1] * wp) << 16);
+        const uint32_t h23 = (uint32_t)float_to_bf16_bits(acc[mt][2] * wp) |
+                             ((uint32_t)float_to_bf16_bits(acc[mt][3] * wp) << 16);
+        *(uint2*)(row + cur.h0 + 4 * g) = uint2{h01, h23};
       }
     }
     if (it_n >= items) break;
@@ -484,7 +483,7 @@ hipError_t launch_gemm1_stream(const uint8_t* hs, const float* hs_scale, const u
 
 hipError_t launch_gemm2_stream(const uint16_t* C, const uint8_t* w2, const float* s2,
                                const int32_t* counts, const int32_t* offsets,
-                               const float* sorted_w, float* partial, int H, int I, int E_l,
+                               const float* sorted_w, Gemm2Out dst, int H, int I, int E_l,
                                int max_pairs, int mt, hipStream_t stream) {
   const int nkb = I / kBlock;
 #define JG_G2S(MT, D)                                                                          \
@@ -493,7 +492,7 @@ hipError_t launch_gemm2_stream(const uint16_t* C, const uint8_t* w2, const float
     const int grid = persistent_grid(groups_per_cu(kWavesPerGroup * D * kWBlk),                \
                                      (waves + kWavesPerGroup - 1) / kWavesPerGroup);            \
     gemm2_stream_kernel<MT, D><<<grid, kWavesPerGroup * kWave, 0, stream>>>(                   \
-        C, w2, s2, counts, offsets, sorted_w, partial, H, I, E_l, max_pairs);                  \
+        C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs);                  \
     return hipGetLastError();                                                                  \
   }
   const int d = ring_depth(nkb, mt == 1 ? JG_G2_STREAM_D : mt == 2 ? 4 : 2);

@@ -249,5 +249,6 @@ def workspace_views(geom: Geometry, T: int, ws: torch.Tensor) -> dict:
         sorted_tok=view("sorted_tok", torch.int32, (Np,)),
         sorted_w=view("sorted_w", torch.float32, (Np,)),
         C=view("C", torch.bfloat16, (Np, geom.intermediate)),
-        partial=view("partial", torch.float32, (Np, geom.hidden)),
+        partial=view("partial", torch.bfloat16, (T * (min(K, El) - 1), geom.hidden)),
+        pair_dst=view("pair_dst", torch.int32, (Np,)),
     )

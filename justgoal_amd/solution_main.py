@@ -73,7 +73,7 @@ def _lib():
         L.moe_run.argtypes = [P] * 8 + [I, ctypes.c_float, P, P, I, P]
         L.moe_run.restype = I
         L.moe_workspace_bytes.argtypes = [I]
-        L.moe_workspace_bytes.restype = ctypes.c_int64
+        L.moe_workspace_bytes.restype = I
         L.moe_error_string.argtypes = [I]
         L.moe_error_string.restype = ctypes.c_char_p
         _LIB = L
@@ -123,7 +123,11 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     # calls that may overlap, on different streams, get different buffers)
     stream = torch.cuda.current_stream(dev)
     key = (dev, int(stream.cuda_stream))
-    need = max(int(L.moe_workspace_bytes(T)), 1)
+    need = int(L.moe_workspace_bytes(T))
+    if need < 0:
+        raise ValueError(f"moe_workspace_bytes({T}) failed ({need}): "
+                         f"{L.moe_error_string(need).decode()}")
+    need = max(need, 1)
     ws = _WS.get(key)
     if ws is None or ws.numel() < need:
         ws = _WS[key] = torch.empty(need, dtype=torch.uint8, device=dev)

@@ -146,7 +146,30 @@ def permute(topk_idx, topk_w, local_offset: int, E_local: int):
     if n < 0:
         raise ValueError("oracle permute rejected the geometry")
     return dict(counts=counts, offsets=offsets, sorted_tok=st[:n].copy(), sorted_w=sw[:n].copy(),
-                pair_of=pair_of)
+                pair_of=pair_of, pair_dst=pair_destinations(idx, pair_of, local_offset, E_local))
+
+
+def pair_destinations(topk_idx, pair_of, local_offset: int, E_local: int):
+    """GEMM2 destination of each pair (this build's layout; the reference accumulates into its
+    output with atomics, opus-4.8 main.py:188-189, and has no such table).
+
+    A token's local pairs, taken in ascending local-expert order, get ranks j = 0, 1, ...: rank 0
+    is written straight into output row t (code t), rank j >= 1 into partial row
+    t * (k - 1) + j - 1 (code -1 - that row), k = min(top_k, E_local). Returns int32 [N] indexed by
+    pair row."""
+    idx = np.asarray(topk_idx, np.int64)
+    T, K = idx.shape
+    k = min(K, E_local)
+    le = idx - int(local_offset)
+    local = (le >= 0) & (le < E_local)
+    # rank of slot (t, a) = local slots b of t with a smaller local expert
+    rank = (local[:, None, :] & (le[:, None, :] < le[:, :, None])).sum(axis=2)
+    t = np.broadcast_to(np.arange(T)[:, None], (T, K))
+    code = np.where(rank == 0, t, -1 - (t * (k - 1) + rank - 1))
+    n = int(local.sum())
+    dst = np.zeros(n, np.int32)
+    dst[np.asarray(pair_of)[local]] = code[local]
+    return dst
 
 
 def quantize_activations(x: torch.Tensor):

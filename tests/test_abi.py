@@ -31,11 +31,26 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_bytes_matches_layout():
     L = _lib.lib()
-    for T in (0, 1, 64, 16384):
+    for T in (0, 1, 64, 901, 11948, 14107, 16107):
         n = L.moe_workspace_bytes(T)
+        assert 0 <= n < 2**31
         assert n == _lib.workspace_layout(DS_V3, T)["total"]
-    # 16384 tokens need more than INT_MAX bytes: the int64 return carries it
-    assert L.moe_workspace_bytes(16384) > 2**31
+    # past 16107 tokens the size no longer fits the int return: an error code, not a wrapped size
+    assert L.moe_workspace_bytes(16108) == -1
+    assert L.moe_workspace_bytes(16384) == -1
+    g = DS_V3.c_struct()
+    assert L.moe_workspace_bytes_ex(ctypes.byref(g), 16384) == _lib.workspace_layout(DS_V3, 16384)["total"]
+
+
+def test_workspace_bytes_as_the_reference_binds_it():
+    """kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t1/main.py:64-65 binds the query as
+    ``argtypes = [c_int]; restype = c_int``; through that binding every token count of the
+    definition's workload list (up to 14107) must give the true size."""
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    L.moe_workspace_bytes.argtypes = [ctypes.c_int]
+    L.moe_workspace_bytes.restype = ctypes.c_int
+    for T in (1, 7, 16, 64, 901, 4096, 11948, 14107):
+        assert L.moe_workspace_bytes(T) == _lib.workspace_layout(DS_V3, T)["total"]
 
 
 def test_layout_regions_ordered_and_aligned():
@@ -43,9 +58,11 @@ def test_layout_regions_ordered_and_aligned():
     offs = [lay[n] for n in _lib.WS_REGIONS] + [lay["total"]]
     assert offs == sorted(offs)
     assert all(o % 256 == 0 for o in offs)
-    # C region holds Np x I bf16
+    # C region holds Np x I bf16, partial T x (k - 1) x H bf16, pair_dst Np int32
     Np = 1000 * 8
     assert lay["partial"] - lay["C"] >= Np * QWEN3.intermediate * 2
+    assert lay["chunk_counts"] - lay["partial"] >= 1000 * 7 * QWEN3.hidden * 2
+    assert lay["total"] - lay["pair_dst"] >= Np * 4
 
 
 @pytest.mark.parametrize("bad", [

@@ -56,9 +56,26 @@ def test_kernel_family_thresholds_match_the_library_source():
     src = open(os.path.join(ROOT, "justgoal_amd", "csrc", "moe_gemm.hip")).read()
     stream = int(re.search(r"#define JG_STREAM_MAX_ROWS (\d+)", src).group(1))
     big = int(re.search(r"#define JG_BIG_ROWS (\d+)", src).group(1))
+    g2 = int(re.search(r"#define JG_G2_STREAM_MAX_ROWS (\d+)", src).group(1))
     assert (bench.GEMM1_STREAM_MAX_ROWS, bench.GEMM1_BIG_ROWS) == (stream, big)
+    assert bench.GEMM2_STREAM_MAX_ROWS == g2
     from justgoal_amd import inputs as jin
     names = {n: bench.gemm1_kernel_name(c) for n, c in jin.CONFIGS.items()}
     assert names["ds_t64"] == "gemm1_stream_kernel"
     assert names["ds_t512"] == "gemm1_tile_kernel"
     assert names["ds_t4096"] == "gemm1_big_kernel"
+
+
+def test_gemm2_unit_figures_and_roofline_bound():
+    # GEMM2: 2*I*H FLOPs per pair; W2 + S2 per active expert, bf16 C read and one bf16 row
+    # written per pair
+    f, b = bench.gemm2_algorithmic(DS_V3, 55, 16)
+    assert f == 55 * 2 * 2048 * 7168
+    assert b == 16 * (7168 * 2048 + 4 * 56 * 16) + 55 * 2048 * 2 + 55 * 7168 * 2
+    # 55 pairs: bytes dominate (HBM); 68197 pairs: FLOPs dominate (MFMA)
+    r = bench.roofline_block("gemm2", "k", 0.05, f, b, bench.PEAK_BF16_TFLOPS, "none")
+    assert r["bound"] == "hbm" and abs(r["achieved"] - b / 0.05e-3 / 1e9) < 1e-6
+    f, b = bench.gemm2_algorithmic(DS_V3, 68197, 23)
+    r = bench.roofline_block("gemm2", "k", 2.0, f, b, bench.PEAK_BF16_TFLOPS, "none")
+    assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s"
+    assert abs(r["frac"] - f / 2e-3 / 1e12 / 2500.0) < 1e-9

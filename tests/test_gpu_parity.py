@@ -93,6 +93,7 @@ def check_case(geom, T, device, seed=0, tokens_checked=None, local_offset=0, bia
     np.testing.assert_array_equal(ws["sorted_w"][:n].cpu().numpy().view(np.uint32),
                                   perm["sorted_w"].view(np.uint32))
     np.testing.assert_array_equal(ws["pair_of"].cpu().numpy(), perm["pair_of"])
+    np.testing.assert_array_equal(ws["pair_dst"][:n].cpu().numpy(), perm["pair_dst"])
 
     # output
     if tokens_checked is None:
@@ -421,6 +422,7 @@ def test_route_entry_matches_oracle(gpu, geom, T, off):
     for k in ("counts", "offsets", "pair_of"):
         np.testing.assert_array_equal(v[k].cpu().numpy(), p[k])
     n = int(p["offsets"][-1])
+    np.testing.assert_array_equal(v["pair_dst"][:n].cpu().numpy(), p["pair_dst"])
     np.testing.assert_array_equal(v["sorted_tok"][:n].cpu().numpy(), p["sorted_tok"])
     np.testing.assert_array_equal(v["sorted_w"][:n].cpu().numpy().view(np.uint32),
                                   p["sorted_w"].view(np.uint32))

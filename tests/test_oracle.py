@@ -179,6 +179,18 @@ def test_permute_invariants(off):
                 assert p["offsets"][le[t, k]] <= q < p["offsets"][le[t, k] + 1]
             else:
                 assert q == -1
+    # destinations, by a per-token loop: the token's local pairs sorted by expert go to output
+    # row t, then to partial rows t*(k-1), t*(k-1)+1, ...; every destination is used once
+    k = min(K, geom.local_experts)
+    seen = set()
+    for t in range(T):
+        mine = sorted((le[t, a], p["pair_of"][t, a]) for a in range(K) if local[t, a])
+        for j, (_, q) in enumerate(mine):
+            d = int(p["pair_dst"][q])
+            assert d == (t if j == 0 else -1 - (t * (k - 1) + j - 1))
+            assert d not in seen
+            seen.add(d)
+    assert len(p["pair_dst"]) == int(local.sum())
 
 
 def test_dequant_layouts():
