@@ -26,7 +26,7 @@ namespace jgmoe {
 namespace {
 
 constexpr int kRouteWaves = 16;          // most tokens per routing workgroup (one wave each)
-// Routing is VALU-throughput-bound (fp64 sigmoid, DPP top-k chains): small batches use 4-token
+// Routing is VALU-latency-bound (sigmoid, DPP top-k chains): small batches use 4-token
 // workgroups so their tokens spread over more CUs; larger ones keep 16 per workgroup so the
 // permute kernel has fewer count rows to sum.
 constexpr int kRouteSmallT = 256, kRouteWavesSmall = 4;
@@ -65,6 +65,53 @@ __device__ __forceinline__ float group_partner(float v, int off) {
   }
 }
 
+// exp and sigmoid in fp32, step for step as the CPU oracle states them (oracle_sigmoid_f32):
+// Cody-Waite range reduction (n = rint(y log2 e), r = y - n ln2 with a 16-bit ln2 head and its
+// tail), e^r = 1 + r q(r) with q the degree-6 Taylor series of (e^r - 1) / r, and the rounding
+// error of that last step kept as a low part; sigmoid = 1 / (1 + e^-x) with 1 + e^-x as a
+// two-float sum and one Newton step on the correctly rounded reciprocal. Every product that
+// feeds an add is an explicit fma, so contraction cannot change the bits. Within 1 ulp of the
+// correctly rounded sigmoid.
+__device__ __forceinline__ float exp_parts(float y, float& lo, int& n) {
+  constexpr float kL2E = 1.44269504088896341f, kLn2Hi = 0.693145751953125f,
+                  kLn2Lo = 1.428606765330187045e-06f;
+  y = fminf(fmaxf(y, -104.0f), 88.0f);
+  const float nf = rintf(y * kL2E);
+  float r = __builtin_fmaf(-nf, kLn2Hi, y);
+  r = __builtin_fmaf(-nf, kLn2Lo, r);
+  float q = 1.0f / 5040.0f;
+  q = __builtin_fmaf(q, r, 1.0f / 720.0f);
+  q = __builtin_fmaf(q, r, 1.0f / 120.0f);
+  q = __builtin_fmaf(q, r, 1.0f / 24.0f);
+  q = __builtin_fmaf(q, r, 1.0f / 6.0f);
+  q = __builtin_fmaf(q, r, 0.5f);
+  q = __builtin_fmaf(q, r, 1.0f);
+  const float h = __builtin_fmaf(r, q, 1.0f);
+  lo = __builtin_fmaf(r, q, 1.0f - h);
+  n = (int)nf;
+  return h;
+}
+
+__device__ __forceinline__ float exp_f32(float y) {
+  float lo;
+  int n;
+  const float h = exp_parts(y, lo, n);
+  return ldexpf(h, n);
+}
+
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  const bool tiny = x < -87.0f;  // 1 + e^-x equals e^-x far below an ulp: the result is e^x
+  float pl;
+  int n;
+  const float ph = exp_parts(tiny ? x : -x, pl, n);
+  const float eh = ldexpf(ph, n), el = ldexpf(pl, n);
+  const float dh = 1.0f + eh;
+  const float dl = (eh >= 1.0f ? (eh - dh) + 1.0f : (1.0f - dh) + eh) + el;
+  const float s0 = 1.0f / dh;
+  const float res = __builtin_fmaf(-s0, dl, __builtin_fmaf(-s0, dh, 1.0f));
+  return tiny ? eh : __builtin_fmaf(s0, res, s0);
+}
+
 __device__ __forceinline__ uint32_t order_key(float v) {
   return float_order_key(v + 0.0f);  // -0 -> +0 so that equal values tie on the index
 }
@@ -83,7 +130,7 @@ __device__ __forceinline__ void route_token(const float (&x)[VPL], const float (
     float v[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      s[j] = (float)(1.0 / (1.0 + exp(-(double)x[j])));
+      s[j] = sigmoid_f32(x[j]);
       v[j] = s[j] + bv[j];
     }
     // top-2 (as a multiset) of this lane's values, then across the group's lanes
@@ -173,7 +220,7 @@ __device__ __forceinline__ void route_token(const float (&x)[VPL], const float (
     float sum = 0.0f;
 #pragma unroll
     for (int k = 0; k < kMaxTopK; ++k) {
-      ex[k] = (float)exp((double)(sel_val[k] - sel_val[0]));
+      ex[k] = exp_f32(sel_val[k] - sel_val[0]);
       if (k < top_k) sum += ex[k];
     }
 #pragma unroll

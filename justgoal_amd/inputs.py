@@ -98,16 +98,23 @@ def make_weights(geom: Geometry, seed: int = 0, device="cpu", experts: int | Non
     return w13, s13, w2, s2
 
 
-def make_activations(geom: Geometry, T: int, seed: int = 0, device="cpu", skew_experts: int = 0,
-                     skew_offset: float = 0.0, local_offset: int = 0):
+def make_routing_inputs(geom: Geometry, T: int, seed: int = 0, skew_experts: int = 0,
+                        skew_offset: float = 0.0, local_offset: int = 0):
+    """(logits fp32 [T, E], bias bf16 [E]) exactly as ``make_activations`` draws them."""
     # one generator per tensor, so the bias does not depend on T
     g_bias = torch.Generator().manual_seed(seed * 7919 + 1)
     g_logits = torch.Generator().manual_seed(seed * 7919 + 2)
-    g_hs = torch.Generator().manual_seed(seed * 7919 + 3)
     bias = (torch.randn(geom.num_experts, generator=g_bias) * 0.1).to(torch.bfloat16)
     logits = torch.randn(T, geom.num_experts, generator=g_logits)
     if skew_experts:
         logits[:, local_offset:local_offset + skew_experts] += skew_offset
+    return logits, bias
+
+
+def make_activations(geom: Geometry, T: int, seed: int = 0, device="cpu", skew_experts: int = 0,
+                     skew_offset: float = 0.0, local_offset: int = 0):
+    logits, bias = make_routing_inputs(geom, T, seed, skew_experts, skew_offset, local_offset)
+    g_hs = torch.Generator().manual_seed(seed * 7919 + 3)
     hs_bf16 = torch.randn(T, geom.hidden, generator=g_hs).to(torch.bfloat16)
     hs, hs_scale = quantize_rows_1x128(hs_bf16)
     return dict(routing_logits=logits.to(device), routing_bias=bias.to(device),

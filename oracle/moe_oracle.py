@@ -51,12 +51,88 @@ def oracle_lib():
                                        P, P, P, P, P]
         for f in (lib.oracle_route_ds, lib.oracle_route_softmax, lib.oracle_permute):
             f.restype = ctypes.c_int
+        for f in (lib.oracle_sigmoid_batch, lib.oracle_exp_batch):
+            f.argtypes = [P, P, ctypes.c_int64]
+            f.restype = None
         _LIB = lib
     return _LIB
 
 
 def _ptr(a: np.ndarray):
     return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def sigmoid_f32(x) -> np.ndarray:
+    """R1 as the C oracle computes it (oracle_sigmoid_f32), element-wise over fp32 ``x``."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    oracle_lib().oracle_sigmoid_batch(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def exp_f32(x) -> np.ndarray:
+    """The C oracle's fp32 exp (oracle_exp_f32), element-wise."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    oracle_lib().oracle_exp_batch(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def fma32(a, b, c) -> np.ndarray:
+    """Correctly rounded fp32 fused multiply-add on arrays, in numpy: the fp64 product of two
+    fp32 values is exact, TwoSum gives the exact sum as s + err, and rounding s to fp32 is
+    corrected where s sits exactly on a rounding midpoint and err breaks the tie."""
+    a, b, c = (np.asarray(v, np.float32).astype(np.float64) for v in (a, b, c))
+    p = a * b
+    s = p + c
+    bb = s - p
+    err = (p - (s - bb)) + (c - bb)
+    r = s.astype(np.float32)
+    rd = r.astype(np.float64)
+    # the other fp32 neighbour of s, on the far side of r
+    other = np.where(s > rd, np.nextafter(r, np.float32(np.inf)),
+                     np.nextafter(r, np.float32(-np.inf))).astype(np.float64)
+    mid = (s != rd) & ((s - rd) == (other - s)) & (err != 0)
+    fix = mid & (np.sign(err) == np.sign(other - rd))
+    return np.where(fix, other.astype(np.float32), r).astype(np.float32)
+
+
+def _exp_parts_numpy(y):
+    f = np.float32
+    y = np.minimum(np.maximum(np.asarray(y, f), f(-104.0)), f(88.0))
+    n = np.rint((y * f(1.44269504088896341)).astype(f))
+    r = fma32(-n, f(0.693145751953125), y)
+    r = fma32(-n, f(1.428606765330187045e-06), r)
+    q = np.full_like(r, f(1.0) / f(5040.0))
+    for c in (f(1.0) / f(720.0), f(1.0) / f(120.0), f(1.0) / f(24.0), f(1.0) / f(6.0), f(0.5),
+              f(1.0)):
+        q = fma32(q, r, c)
+    h = fma32(r, q, f(1.0))
+    lo = fma32(r, q, (f(1.0) - h).astype(f))
+    return h, lo, n.astype(np.int32)
+
+
+def sigmoid_numpy(x) -> np.ndarray:
+    """Independent numpy statement of oracle_sigmoid_f32 (same steps, fma emulated exactly)."""
+    f = np.float32
+    x = np.asarray(x, f)
+    small = x < f(-87.0)
+    ph, pl, n = _exp_parts_numpy(np.where(small, x, -x))
+    eh = np.ldexp(ph, n).astype(f)
+    el = np.ldexp(pl, n).astype(f)
+    dh = (f(1.0) + eh).astype(f)
+    dl = (np.where(eh >= f(1.0), ((eh - dh).astype(f) + f(1.0)).astype(f),
+                   ((f(1.0) - dh).astype(f) + eh).astype(f)) + el).astype(f)
+    with np.errstate(divide="ignore"):
+        s0 = (f(1.0) / dh).astype(f)
+    res = fma32(-s0, dl, fma32(-s0, dh, f(1.0)))
+    out = fma32(s0, res, s0)
+    return np.where(small, eh, out).astype(f)
+
+
+def exp_numpy(y) -> np.ndarray:
+    ph, _, n = _exp_parts_numpy(y)
+    return np.ldexp(ph, n).astype(np.float32)
 
 
 def route(logits, bias, geom, rsf: float):
@@ -92,7 +168,7 @@ def route_numpy(logits, bias, geom, rsf: float):
     K = geom.top_k
     order_idx = np.arange(E)
     if geom.routing_method == ROUTING_DS:
-        s = (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+        s = sigmoid_numpy(x)
         b = (np.zeros(E, np.float32) if bias is None
              else torch.as_tensor(bias).to(torch.bfloat16).float().cpu().numpy())
         v = (s + b[None, :]).astype(np.float32)
@@ -119,7 +195,7 @@ def route_numpy(logits, bias, geom, rsf: float):
         idx = eorder[:, :K].astype(np.int32)
         xs = np.take_along_axis(x, idx, axis=1)
         d = (xs - xs[:, :1]).astype(np.float32)
-        ex = np.exp(d.astype(np.float64)).astype(np.float32)
+        ex = exp_numpy(d)
         tot = np.zeros(T, np.float32)
         for k in range(K):
             tot = (tot + ex[:, k]).astype(np.float32)

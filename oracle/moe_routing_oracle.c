@@ -31,8 +31,14 @@
  *
  * Precision conventions this oracle fixes (the kernels follow them exactly, so indices and
  * weights are bit-identical):
- *   - sigmoid and exp are evaluated in double and rounded once to fp32 (correctly rounded
- *     except in astronomically rare cases); the reference's fp32 sigmoid agrees within 1 ulp.
+ *   - R1 is an fp32 sigmoid built from the steps of sigmoid_f32 below (Cody-Waite range
+ *     reduction and a Taylor polynomial for exp, carried as a two-float value, then a
+ *     Newton-corrected reciprocal of 1 + e^-x). Every step is an IEEE fp32 operation (fmaf
+ *     where a product feeds an add, correctly rounded division, ldexpf), so the GPU gives the
+ *     same bits. It is within 1 ulp of the correctly rounded sigmoid and within 2 ulp of
+ *     torch.sigmoid (tests/test_oracle.py); the reference's 1/(1+expf(-x)) is an fp32 sigmoid
+ *     of the same kind.
+ *   - softmax weights use exp_f32 (the high part of the same exp) of x_k - x_max.
  *   - the selected-s sum is accumulated in selection order (descending v, ties lower index),
  *     in fp32, starting from 0.0f; then 1e-20f is added; w = (s / sum) * rsf in fp32.
  */
@@ -47,7 +53,67 @@ static float bf16_to_float(uint16_t b) {
   return f;
 }
 
-static float sigmoid_rn(float x) { return (float)(1.0 / (1.0 + exp(-(double)x))); }
+/*
+ * exp(y) = 2^n (ph + pl), |pl| <= ulp(ph): n = rint(y log2 e), r = y - n ln2 in two steps
+ * (Cody-Waite: LN2_HI has 16 significant bits, LN2_LO = ln2 - LN2_HI), e^r = 1 + r q(r) with q
+ * the Taylor series of (e^r - 1) / r to degree 6 (truncation < 2^-27 for |r| <= ln2 / 2), and
+ * the rounding error of the final 1 + r q recovered exactly by a second fma. y is clamped to
+ * [-104, 88], where e^y stays finite.
+ */
+static const float kL2E = 1.44269504088896341f;
+static const float kLn2Hi = 0.693145751953125f;
+static const float kLn2Lo = 1.428606765330187045e-06f;
+
+static void exp_parts(float y, float* ph, float* pl, int* n_out) {
+  y = fminf(fmaxf(y, -104.0f), 88.0f);
+  const float n = rintf(y * kL2E);
+  float r = fmaf(-n, kLn2Hi, y);
+  r = fmaf(-n, kLn2Lo, r);
+  float q = 1.0f / 5040.0f;
+  q = fmaf(q, r, 1.0f / 720.0f);
+  q = fmaf(q, r, 1.0f / 120.0f);
+  q = fmaf(q, r, 1.0f / 24.0f);
+  q = fmaf(q, r, 1.0f / 6.0f);
+  q = fmaf(q, r, 0.5f);
+  q = fmaf(q, r, 1.0f);
+  const float h = fmaf(r, q, 1.0f);
+  *ph = h;
+  *pl = fmaf(r, q, 1.0f - h); /* 1 - h is exact (h in [0.70, 1.42]) */
+  *n_out = (int)n;
+}
+
+float oracle_exp_f32(float y) {
+  float ph, pl;
+  int n;
+  exp_parts(y, &ph, &pl, &n);
+  return ldexpf(ph, n);
+}
+
+/*
+ * sigmoid(x) = 1 / d with d = 1 + e^-x held as dh + dl (Fast2Sum of 1 and the high part, plus
+ * the low part), s0 = RN(1 / dh), then one Newton step s0 + s0 (1 - s0 dh - s0 dl). Below
+ * x = -87, 1 + e^-x equals e^-x to far below an ulp and the result is e^x.
+ */
+float oracle_sigmoid_f32(float x) {
+  float ph, pl;
+  int n;
+  exp_parts(x < -87.0f ? x : -x, &ph, &pl, &n);
+  if (x < -87.0f) return ldexpf(ph, n);
+  const float eh = ldexpf(ph, n), el = ldexpf(pl, n);
+  const float dh = 1.0f + eh;
+  const float dl = (eh >= 1.0f ? (eh - dh) + 1.0f : (1.0f - dh) + eh) + el;
+  const float s0 = 1.0f / dh;
+  const float res = fmaf(-s0, dl, fmaf(-s0, dh, 1.0f));
+  return fmaf(s0, res, s0);
+}
+
+/* Batch forms for the pinning tests. */
+void oracle_sigmoid_batch(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = oracle_sigmoid_f32(x[i]);
+}
+void oracle_exp_batch(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = oracle_exp_f32(x[i]);
+}
 
 /* Returns 1 if (va, ia) ranks before (vb, ib): larger value first, ties -> lower index. */
 static int better(float va, int ia, float vb, int ib) { return va > vb || (va == vb && ia < ib); }
@@ -68,7 +134,7 @@ int oracle_route_ds(const float* logits, const uint16_t* bias, int T, int E, int
   for (int t = 0; t < T; ++t) {
     const float* x = logits + (size_t)t * E;
     for (int e = 0; e < E; ++e) {
-      s[e] = sigmoid_rn(x[e]);
+      s[e] = oracle_sigmoid_f32(x[e]);
       v[e] = s[e] + (bias ? bf16_to_float(bias[e]) : 0.0f);
     }
     for (int g = 0; g < n_group; ++g) {
@@ -128,7 +194,7 @@ int oracle_route_softmax(const float* logits, int T, int E, int top_k, int32_t* 
     }
     float ex[64], sum = 0.0f;
     for (int k = 0; k < top_k; ++k) {
-      ex[k] = (float)exp((double)(xs[k] - xs[0]));
+      ex[k] = oracle_exp_f32(xs[k] - xs[0]);
       sum += ex[k];
     }
     for (int k = 0; k < top_k; ++k) topk_w[(size_t)t * top_k + k] = ex[k] / sum;

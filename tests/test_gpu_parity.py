@@ -57,8 +57,30 @@ def subset_tokens(inp_cpu, tok):
     return d
 
 
+def tile_covering_tokens(perm, bm=128, seed=0, extra=64):
+    """Tokens whose rows, between them, touch every M-tile of both GEMMs: for each expert
+    segment and each bm-pair tile of it (the large-tile kernels use bm = 128; the smaller tiles
+    of the other kernels nest inside), the tokens of its first and last pair; plus ``extra``
+    random tokens. A fault confined to one tile shows up in at least one checked row."""
+    off = perm["offsets"]
+    st = perm["sorted_tok"]
+    tok = set()
+    for e in range(len(off) - 1):
+        for p0 in range(int(off[e]), int(off[e + 1]), bm):
+            p1 = min(p0 + bm, int(off[e + 1])) - 1
+            tok.add(int(st[p0]))
+            tok.add(int(st[p1]))
+    T = int(perm["pair_of"].shape[0])
+    rng = np.random.default_rng(seed)
+    tok.update(int(t) for t in rng.choice(T, size=min(T, extra), replace=False))
+    return np.array(sorted(tok))
+
+
 def check_case(geom, T, device, seed=0, tokens_checked=None, local_offset=0, bias=True,
-               skew=(0, 0.0), rsf=None, logits=None):
+               skew=(0, 0.0), rsf=None, logits=None, runner=None):
+    """Runs the operator (``run``, or ``runner(inputs_on_device) -> (out, workspace)``) and
+    compares routing/permute bit for bit and the output within tolerance. ``tokens_checked``:
+    None = every token, an int = that many random tokens, "tiles" = tile_covering_tokens."""
     (w_cpu, w_dev) = weights_for(geom, device)
     act = jin.make_activations(geom, T, seed=seed, skew_experts=skew[0], skew_offset=skew[1],
                                local_offset=local_offset)
@@ -76,9 +98,13 @@ def check_case(geom, T, device, seed=0, tokens_checked=None, local_offset=0, bia
                    local_expert_offset=local_offset,
                    routed_scaling_factor=inp_cpu["routed_scaling_factor"])
     say(f"[case] geom={geom.name} T={T} seed={seed} off={local_offset} bias={bias} skew={skew}")
-    out = run(**inp_dev, geometry=geom)
+    if runner is None:
+        out = run(**inp_dev, geometry=geom)
+        ws_buf = workspace(geom, T, device)
+    else:
+        out, ws_buf = runner(inp_dev)
     torch.cuda.synchronize()
-    ws = workspace_views(geom, T, workspace(geom, T, device))
+    ws = workspace_views(geom, T, ws_buf)
 
     # routing + permute: bit-exact against the oracle over all T tokens
     idx, w = oracle.route(inp_cpu["routing_logits"], inp_cpu["routing_bias"], geom,
@@ -99,6 +125,10 @@ def check_case(geom, T, device, seed=0, tokens_checked=None, local_offset=0, bia
     if tokens_checked is None:
         tok = np.arange(T)
         ref = oracle.moe_reference(inp_cpu, geom)
+    elif tokens_checked == "tiles":
+        tok = tile_covering_tokens(perm, seed=seed)
+        say(f"  checking {len(tok)} tile-covering tokens")
+        ref = oracle.moe_reference(subset_tokens(inp_cpu, tok), geom)
     else:
         rng = np.random.default_rng(seed)
         tok = np.sort(rng.choice(T, size=min(T, tokens_checked), replace=False))
@@ -168,17 +198,64 @@ def test_ds_config1_t64(gpu):
 
 
 def test_ds_config2_t4096(gpu):
-    check_case(DS_V3, 4096, gpu, seed=0, tokens_checked=256)
+    check_case(DS_V3, 4096, gpu, seed=0)  # every token
 
 
 def test_ds_config3_t16384_skew(gpu):
-    out, ws = check_case(DS_V3, 16384, gpu, seed=0, tokens_checked=96, skew=(8, 3.0))
+    out, ws = check_case(DS_V3, 16384, gpu, seed=0, tokens_checked="tiles", skew=(8, 3.0))
     c = ws["counts"].cpu().numpy()
     assert c[:8].sum() > 0.5 * c.sum()   # the boosted experts take most of the local pairs
 
 
 def test_qwen3_config4_t1024(gpu):
-    check_case(QWEN3, 1024, gpu, seed=0, tokens_checked=256)
+    check_case(QWEN3, 1024, gpu, seed=0)  # every token
+
+
+def reference_binding():
+    """The library bound exactly as the reference's ctypes loader binds its CUDA build
+    (kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t1/main.py:60-65): c_int workspace
+    size, c_int return code."""
+    import ctypes
+    from justgoal_amd import _lib
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    lib.moe_run.restype = ctypes.c_int
+    lib.moe_run.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p,
+                                                  ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.moe_workspace_bytes.restype = ctypes.c_int
+    lib.moe_workspace_bytes.argtypes = [ctypes.c_int]
+    return lib
+
+
+def reference_style_runner(device):
+    lib = reference_binding()
+
+    def runner(d):
+        T = int(d["routing_logits"].shape[0])
+        n = lib.moe_workspace_bytes(T)
+        assert n > 0
+        ws = torch.zeros(n, dtype=torch.uint8, device=device)  # as t1/main.py:77-83 allocates it
+        out = torch.empty((T, DS_V3.hidden), dtype=torch.bfloat16, device=device)
+        rc = lib.moe_run(d["routing_logits"].data_ptr(), d["routing_bias"].data_ptr(),
+                         d["hidden_states"].data_ptr(), d["hidden_states_scale"].data_ptr(),
+                         d["gemm1_weights"].data_ptr(), d["gemm1_weights_scale"].data_ptr(),
+                         d["gemm2_weights"].data_ptr(), d["gemm2_weights_scale"].data_ptr(),
+                         int(d["local_expert_offset"]), float(d["routed_scaling_factor"]),
+                         out.data_ptr(), ws.data_ptr(), T,
+                         torch.cuda.current_stream(device).cuda_stream)
+        assert rc == 0, rc
+        return out, ws
+
+    return runner
+
+
+# The definition's own token counts (goal_full_shape/opus-5/moe_fp8_fwd/
+# moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048/main.py:1219-1221) that no other
+# test uses, through the reference's binding; the two largest need the int
+# workspace size to hold 1.59 GB and 1.88 GB.
+@pytest.mark.parametrize("T", [901, 11948, 14107])
+def test_definition_token_counts_via_reference_binding(gpu, T):
+    say(f"reference binding: DS-V3 T={T}")
+    check_case(DS_V3, T, gpu, seed=T, tokens_checked="tiles", runner=reference_style_runner(gpu))
 
 
 # Qwen3 geometry (H=4096, I=1536: 12 K blocks in GEMM2) across the kernel families:

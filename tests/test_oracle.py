@@ -56,7 +56,7 @@ def _brute_route_ds(x, b, geom, rsf):
     candidates beat it, where a beats b if its value is larger or equal with a lower index."""
     T, E = x.shape
     gs = E // geom.n_group
-    s = (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+    s = oracle.sigmoid_numpy(x)
     v = (s + b[None, :]).astype(np.float32)
     out_idx = np.zeros((T, geom.top_k), np.int64)
     for t in range(T):
@@ -127,7 +127,7 @@ def test_routing_against_torch_topk_and_sigmoid():
     b = _bias(256, 3)
     idx, w = oracle.route(x, b, geom, 2.5)
     s_ref = torch.sigmoid(x)  # fp32 library sigmoid, within 2 ulp of the correctly rounded one
-    s_or = torch.from_numpy((1.0 / (1.0 + np.exp(-x.double().numpy()))).astype(np.float32))
+    s_or = torch.from_numpy(oracle.sigmoid_f32(x.numpy()))
     ulp = torch.abs(s_ref.view(torch.int32) - s_or.view(torch.int32))
     assert int(ulp.max()) <= 2
     v = s_or + b.float()
@@ -142,6 +142,87 @@ def test_routing_against_torch_topk_and_sigmoid():
     torch.testing.assert_close(torch.from_numpy(w), w_ref, rtol=1e-6, atol=1e-7)
     # invariant: sum of the weights is the scaling factor
     np.testing.assert_allclose(w.sum(1), 2.5, rtol=1e-5)
+
+
+def _ulps(a, b):
+    return np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+
+
+def _float_sample(lo_abs, hi_abs, n):
+    """About n fp32 values of each sign with |x| in [lo_abs, hi_abs], evenly spaced in bit
+    pattern (so every binade is covered), plus the boundary values."""
+    a = np.float32(lo_abs).view(np.int32)
+    b = np.float32(hi_abs).view(np.int32)
+    step = max(1, int(b - a) // n)
+    m = np.arange(a, b, step, dtype=np.int32).view(np.float32)
+    return np.concatenate([m, -m, np.float32([lo_abs, hi_abs, -lo_abs, -hi_abs])])
+
+
+def test_sigmoid_f32_pinned():
+    """R1 (oracle_sigmoid_f32, which the routing kernel restates step for step): within 1 ulp of
+    the correctly rounded sigmoid (fp64 evaluation rounded once) on every binade of |x| in
+    [2^-30, 90], exactly rounded in at least 99% of cases; within 2 ulp of torch.sigmoid
+    (itself up to 2 ulp from the correctly rounded value); identical to the independent numpy
+    statement; and fixed points of the closed form."""
+    x = _float_sample(2.0 ** -30, 90.0, 1_500_000)
+    s = oracle.sigmoid_f32(x)
+    exact = (1.0 / (1.0 + np.exp(-x.astype(np.float64)))).astype(np.float32)
+    d = _ulps(s, exact)
+    assert d.max() <= 1
+    assert (d == 0).mean() > 0.99  # 99.1% on this sample
+    inner = np.abs(x) <= 80  # torch flushes part of the subnormal range beyond
+    assert _ulps(s[inner], torch.sigmoid(torch.from_numpy(x[inner])).numpy()).max() <= 2
+    np.testing.assert_array_equal(s.view(np.uint32), oracle.sigmoid_numpy(x).view(np.uint32))
+    special = np.float32([0.0, -0.0, 88.0, 104.0, 1e30, -87.0, -87.5, -103.0, -104.0, -200.0,
+                          -1e30])
+    got = oracle.sigmoid_f32(special)
+    assert got[0] == 0.5 and got[1] == 0.5
+    assert (got[2:5] == 1.0).all()
+    assert got[-3] == 0.0 and got[-2] == 0.0 and got[-1] == 0.0
+    ref = (1.0 / (1.0 + np.exp(-special[5:8].astype(np.float64)))).astype(np.float32)
+    assert _ulps(got[5:8], ref).max() <= 1
+    # symmetry of the closed form: s(x) + s(-x) = 1 to within an ulp of 1
+    y = x[(np.abs(x) < 16)]
+    np.testing.assert_allclose(oracle.sigmoid_f32(y).astype(np.float64)
+                               + oracle.sigmoid_f32(-y).astype(np.float64), 1.0, atol=2.0 ** -23)
+
+
+def test_exp_f32_pinned():
+    """The softmax weights' exp (oracle_exp_f32): within 1 ulp of the correctly rounded exp on
+    [-87, 0] (softmax arguments x_k - x_max are <= 0), e^0 = 1 exactly, and equal to the numpy
+    statement."""
+    x = -_float_sample(2.0 ** -30, 87.0, 1_000_000)
+    x = x[x <= 0]
+    e = oracle.exp_f32(x)
+    exact = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert _ulps(e, exact).max() <= 1
+    np.testing.assert_array_equal(e.view(np.uint32), oracle.exp_numpy(x).view(np.uint32))
+    assert oracle.exp_f32(np.float32([0.0]))[0] == 1.0
+
+
+def test_fma32_emulation():
+    """The numpy fma used by the numpy statements: exact against fp64 where the fp64 sum is
+    exact, and the midpoint tie-break on constructed cases."""
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal(100000).astype(np.float32)
+    b = rng.standard_normal(100000).astype(np.float32)
+    c = np.ldexp(rng.standard_normal(100000), rng.integers(-30, 30, 100000)).astype(np.float32)
+    got = oracle.fma32(a, b, c)
+    # fp64 products of fp32 are exact; with |c| not far from |ab| the fp64 sum is exact too,
+    # and then one rounding to fp32 is the fused result
+    p = a.astype(np.float64) * b.astype(np.float64)
+    ok = np.abs(np.log2(np.abs(c) + 1e-300) - np.log2(np.abs(p) + 1e-300)) < 4
+    np.testing.assert_array_equal(got[ok], (p + c.astype(np.float64))[ok].astype(np.float32))
+    # 658529 * 104353 = 2^36 + 1, so a*b = 2^-24 + 2^-60 and 1 + a*b lies just above the
+    # midpoint between 1 and 1 + 2^-23: the fused result rounds up, while rounding the fp64 sum
+    # (which drops 2^-60 and lands on the midpoint) and then to fp32 gives 1.0
+    a1 = np.float32(658529 * 2.0 ** -30)
+    b1 = np.float32(104353 * 2.0 ** -30)
+    assert 658529 * 104353 == 2 ** 36 + 1
+    assert (a1.astype(np.float64) * b1 + 1.0).astype(np.float32) == 1.0
+    assert oracle.fma32(a1, b1, np.float32(1.0)) == np.float32(1 + 2.0 ** -23)
+    assert oracle.fma32(-a1, b1, np.float32(-1.0)) == np.float32(-(1 + 2.0 ** -23))
+    assert oracle.fma32(a1, b1, np.float32(-1.0)) == np.float32(-1.0 + 2.0 ** -24)
 
 
 def test_softmax_routing_against_torch():
