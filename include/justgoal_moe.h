@@ -34,6 +34,7 @@ extern "C" {
 #define MOE_ERR_INVALID_ARG (-1)     /* null pointer, negative T, T above the limit, bad scalar */
 #define MOE_ERR_GEOMETRY (-2)        /* geometry the kernels do not support */
 #define MOE_ERR_NO_DEVICE (-3)       /* device query failed or the device is not gfx950 */
+#define MOE_ERR_SCRATCH_SIZE (-4)    /* moe_run_noalloc: the call needs more than its scratch */
 
 #define MOE_ROUTING_DS 0             /* sigmoid + bias, group-limited top-k, renorm x scaling */
 #define MOE_ROUTING_SOFTMAX 1        /* softmax top-k, renormalised */
@@ -83,6 +84,23 @@ int moe_run_ex(const moe_geometry* geom, const void* logits, const void* bias, c
 
 /* Workspace bytes for moe_run_ex; -MOE_ERR_* style negative value on a bad geometry. */
 int64_t moe_workspace_bytes_ex(const moe_geometry* geom, int T);
+
+/*
+ * moe_run_ex without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. It calls no allocator: the workspace is a fixed array of
+ * MOE_NOALLOC_SCRATCH_BYTES in the library's device code, one per GPU, held until the process
+ * ends (its device address is looked up once per device on the first call there). A call whose
+ * moe_workspace_bytes_ex exceeds that size returns MOE_ERR_SCRATCH_SIZE before enqueueing
+ * anything (DS-V3: up to 503 tokens; the Qwen3-style geometry: up to 816). Every call on a GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (other streams, other host
+ * threads) race and must not be issued; calls ordered on one stream are fine.
+ */
+#define MOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int moe_run_noalloc(const moe_geometry* geom, const void* logits, const void* bias,
+                    const void* hs, const void* hs_scale, const void* w13, const void* s13,
+                    const void* w2, const void* s2, int local_offset, float scaling, void* out,
+                    int T, void* stream);
 
 /*
  * Routing + permute stages only (the first two kernels of moe_run_ex), leaving their outputs in

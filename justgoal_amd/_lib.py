@@ -16,7 +16,7 @@ LIB_PATH = os.environ.get("JUSTGOAL_MOE_LIB") or os.path.join(_HERE, "libjustgoa
 # Every symbol include/justgoal_moe.h declares.
 EXPORTED = ("moe_run", "moe_workspace_bytes", "moe_run_ex", "moe_workspace_bytes_ex",
             "moe_route_ex", "moe_workspace_layout", "moe_set_stage_events", "moe_error_string",
-            "moe_quantize_activations")
+            "moe_quantize_activations", "moe_run_noalloc")
 
 MOE_WS_NUM_REGIONS = 11
 WS_REGIONS = ("topk_idx", "topk_w", "pair_of", "counts", "offsets", "sorted_tok", "sorted_w", "C",
@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
         L.moe_workspace_layout.restype = I
         L.moe_set_stage_events.argtypes = [ctypes.POINTER(ctypes.c_void_p), I]
         L.moe_set_stage_events.restype = I
+        L.moe_run_noalloc.argtypes = [G] + [P] * 8 + [I, F, P, I, P]
+        L.moe_run_noalloc.restype = I
         L.moe_quantize_activations.argtypes = [P, I, I, P, P, P]
         L.moe_quantize_activations.restype = I
         L.moe_error_string.argtypes = [I]

@@ -153,6 +153,33 @@ int route_and_permute(const moe_geometry* g, const void* logits, const void* bia
   return MOE_OK;
 }
 
+// Scratch of moe_run_noalloc: one copy of this array per device, allocated by the runtime when
+// the code object is loaded and held until the process ends. In host code `scratch` is only a
+// host-side handle; the device address comes from hipGetSymbolAddress (scratch_ptr below).
+static __device__ __align__(256) uint8_t scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_status[kMaxDevices];
+
+// Device address of this device's scratch array, looked up once per device with that device
+// current. Returns the lookup's error code (and no pointer) if it failed.
+hipError_t scratch_ptr(void** p) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* q = nullptr;
+    g_scratch_status[dev] = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = q;
+  });
+  if (g_scratch_status[dev] != hipSuccess) return g_scratch_status[dev];
+  *p = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
 hipEvent_t g_stage_events[MOE_NUM_STAGES + 1];
 int g_stage_events_on = 0;
 
@@ -251,6 +278,26 @@ int moe_run(const void* logits, const void* bias, const void* hs, const void* hs
                     out, workspace, T, stream);
 }
 
+int moe_run_noalloc(const moe_geometry* geom, const void* logits, const void* bias,
+                    const void* hs, const void* hs_scale, const void* w13, const void* s13,
+                    const void* w2, const void* s2, int local_offset, float scaling, void* out,
+                    int T, void* stream) {
+  int rc = check_geometry(geom);
+  if (rc != MOE_OK) return rc;
+  if (T < 0) return MOE_ERR_INVALID_ARG;
+  if (T == 0) return MOE_OK;
+  int64_t off[MOE_WS_NUM_REGIONS + 1];
+  layout(geom, T, off);
+  if (off[MOE_WS_NUM_REGIONS] > (int64_t)MOE_NOALLOC_SCRATCH_BYTES) return MOE_ERR_SCRATCH_SIZE;
+  if ((rc = check_device()) != MOE_OK) return rc;
+  void* ws = nullptr;
+  JG_TRY(scratch_ptr(&ws));
+  // No region of the workspace has to start at any value (every kernel writes before it reads),
+  // so the scratch array is used as it is, left over from the previous call.
+  return moe_run_ex(geom, logits, bias, hs, hs_scale, w13, s13, w2, s2, local_offset, scaling,
+                    out, ws, T, stream);
+}
+
 int moe_quantize_activations(const void* x, int T, int H, void* q, void* scale, void* stream) {
   if (T < 0 || H <= 0 || H % 128 != 0) return MOE_ERR_INVALID_ARG;
   if (T == 0) return MOE_OK;
@@ -270,6 +317,9 @@ const char* moe_error_string(int rc) {
              "takes)";
     case MOE_ERR_GEOMETRY: return "unsupported MoE geometry";
     case MOE_ERR_NO_DEVICE: return "no gfx950 (MI355X) device is current";
+    case MOE_ERR_SCRATCH_SIZE:
+      return "the call needs more workspace than moe_run_noalloc's fixed scratch array holds "
+             "(use moe_run_ex with a caller workspace)";
     default: return rc > 0 ? hipGetErrorString((hipError_t)rc) : "unknown error";
   }
 }
