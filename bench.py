@@ -40,8 +40,8 @@ PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5000.0
 PEAK_BF16_TFLOPS = 2500.0
 STAGES = ("route", "permute", "gemm1_swiglu", "gemm2", "combine")
-# Kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (JG_STREAM_MAX_ROWS, JG_BIG_ROWS,
-# JG_G2_STREAM_MAX_ROWS defaults; tests/test_bench.py checks they match the source)
+# Kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (kStreamMaxRows, kBigRows,
+# kG2StreamMaxRows; tests/test_bench.py checks they match the source)
 GEMM1_STREAM_MAX_ROWS = 4
 GEMM1_BIG_ROWS = 64
 GEMM2_STREAM_MAX_ROWS = 3

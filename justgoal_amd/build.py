@@ -30,15 +30,11 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False, out: str = LIB_PATH, defines=(), extra_flags=()) -> str:
-    """Compile every source into one shared library; returns its path.
-
-    ``defines`` (e.g. ``["JG_G1_STREAM_D=6"]``) override the kernels' compile-time tuning knobs;
-    the default build uses none."""
+def build(verbose: bool = False, out: str = LIB_PATH) -> str:
+    """Compile every source into one shared library; returns its path."""
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
     tmp = out + f".{os.getpid()}.tmp"
-    cmd = [HIPCC, *FLAGS, f"-I{INCLUDE}", *extra_flags, *[f"-D{d}" for d in defines], "-o", tmp,
-           *srcs]
+    cmd = [HIPCC, *FLAGS, f"-I{INCLUDE}", "-o", tmp, *srcs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

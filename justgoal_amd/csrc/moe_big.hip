@@ -22,9 +22,6 @@
 #include "moe_device.h"
 #include "moe_kernels.h"
 
-#ifndef JG_XCD_MAP
-#define JG_XCD_MAP 0
-#endif
 
 namespace jgmoe {
 
@@ -36,15 +33,40 @@ constexpr int kWBlk = 16 * kBlock;  // 16 rows x 128 bytes
 // A buffer offset past every buffer these kernels address (all are < 2 GiB; the launchers check).
 constexpr uint32_t kOutOfRange = 0x7ffffff0u;
 
-// Optional (JG_XCD_MAP=1; measured mixed: Qwen3 GEMM1 13% faster, DS-V3 T=4096 GEMM1 15% slower, so off).
 // Workgroups are dispatched to the 8 XCDs round-robin (workgroup b runs on XCD b % 8), and the
 // persistent loop hands workgroup b the items b, b + grid, ... (grid a multiple of 8). This
-// bijection on [0, items) gives XCD x a contiguous run of the tile-major item list instead of
-// every 8th item, so the column items of one M-tile (sharing its activation rows) and the M-tiles
-// of one expert (sharing its weights) meet in the same L2.
+// bijection on [0, items) gives XCD x a contiguous run of the logical item list instead of
+// every 8th item, so consecutive logical items meet in the same L2.
 __device__ __forceinline__ int xcd_item(int i, int items) {
   const int x = i & 7, q = items >> 3, r = items & 7;
   return x * q + (x < r ? x : r) + (i >> 3);
+}
+
+// Work item -> (expert, first row m0 of its M-tile, N-tile nt). sched bit 0: XCD-contiguous
+// physical order (xcd_item); sched >> 1 = GM: 0 = tile-major logical order (the N-tiles of one
+// M-tile consecutive), else each expert's M-tiles in bands of GM with the band's items
+// N-tile-major (GM M-tiles of one N-tile consecutive).
+template <int BM>
+__device__ __forceinline__ int map_item(const TileMapLds& tml, int item, int items, int NNT,
+                                        int E_l, int sched, int& m0, int& cnt, int& seg,
+                                        int& nt) {
+  item = uniform((sched & 1) ? xcd_item(item, items) : item);
+  const int tile = item / NNT;
+  const int e = uniform(tml.template find<BM>(tile, E_l, m0, cnt, seg));
+  nt = item - tile * NNT;
+  const int GM = sched >> 1;
+  if (GM > 0) {
+    const int first = tile - uniform(m0) / BM;  // the expert's first tile slot
+    const int me = (uniform(cnt) + BM - 1) / BM;
+    const int local = item - first * NNT;
+    const int band = local / (GM * NNT);
+    const int rows = min(GM, me - band * GM);
+    const int idx = local - band * GM * NNT;
+    nt = idx / rows;
+    m0 = (band * GM + idx % rows) * BM;
+  }
+  nt = uniform(nt);
+  return e;
 }
 
 constexpr int vm_depth(int n) { return n > 63 ? 63 : n < 0 ? 0 : n; }
@@ -80,7 +102,7 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
     const uint8_t* __restrict__ w13, const float* __restrict__ s13,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ sorted_tok, uint16_t* __restrict__ C, int T, int H, int I,
-    int E_l, int max_pairs) {
+    int E_l, int max_pairs, int sched) {
   static_assert(D >= 3, "the prefetch lead is D-1 blocks");
   static_assert(16 * NS <= kBlock && kBlock % (16 * NS) == 0, "a wave's columns share one scale block");
   constexpr int BM = 16 * MS * WM, BN = 16 * NS * WN;
@@ -106,9 +128,8 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
   const int stride = gridDim.x;
 
   auto scalars = [&](int item, B1Scalars& x) {
-    item = uniform(JG_XCD_MAP ? xcd_item(item, items) : item);
-    const int tile = item / NNT, nt = item % NNT;
-    x.e = uniform(tml.template find<BM>(tile, E_l, x.m0, x.cnt, x.seg));
+    int nt;
+    x.e = uniform(map_item<BM>(tml, item, items, NNT, E_l, sched, x.m0, x.cnt, x.seg, nt));
     x.m0 = uniform(x.m0);
     x.cnt = uniform(x.cnt);
     x.seg = uniform(x.seg);
@@ -434,7 +455,8 @@ template <int MS, int NS, int D, int WM, int WN>
 __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
     const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const float* __restrict__ sorted_w, Gemm2Out dst, int H, int I, int E_l, int max_pairs) {
+    const float* __restrict__ sorted_w, Gemm2Out dst, int H, int I, int E_l, int max_pairs,
+    int sched) {
   static_assert(D >= 3, "the prefetch lead is D-1 blocks");
   static_assert(16 * NS <= kBlock && kBlock % (16 * NS) == 0, "a wave's columns share one scale block");
   constexpr int BM = 16 * MS * WM, BN = 16 * NS * WN;
@@ -459,9 +481,8 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
   const int stride = gridDim.x;
 
   auto scalars = [&](int item, B2Scalars& x) {
-    item = uniform(JG_XCD_MAP ? xcd_item(item, items) : item);
-    const int tile = item / NNT, nt = item % NNT;
-    x.e = uniform(tml.template find<BM>(tile, E_l, x.m0, x.cnt, x.seg));
+    int nt;
+    x.e = uniform(map_item<BM>(tml, item, items, NNT, E_l, sched, x.m0, x.cnt, x.seg, nt));
     x.m0 = uniform(x.m0);
     x.cnt = uniform(x.cnt);
     x.seg = uniform(x.seg);
@@ -741,6 +762,16 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
 
 }  // namespace
 
+// Item schedules (map_item). GEMM1: XCD-contiguous physical order over bands of 8 M-tiles,
+// N-tile-major inside a band, so an XCD's 32 concurrent items share W13 panels across up to 8
+// M-tiles and activation rows across 4 N-tiles. Against the tile-major round-robin order it cut
+// GEMM1's HBM fetch at T=4096 from 1.19 to 0.89 GB (algorithmic 0.80) and at T=16384 (skewed)
+// from 7.96 to 6.07 GB, and its time from 364 to 327 us for the Qwen3-style T=1024 batch
+// (T=4096: 222 -> 217 us; T=16384: within 1%). GEMM2 keeps the tile-major round-robin order:
+// every variant tried (XCD-contiguous, bands of 2-16) was 1-5% slower there.
+constexpr int kSchedGemm1 = 1 | (8 << 1);
+constexpr int kSchedGemm2 = 0;
+
 static int big_grid(long long max_items) {
   const int cus = device_cu_count();
   long long g = cus;  // the LDS rings leave room for one workgroup per CU
@@ -752,47 +783,28 @@ static inline long long big_tiles(int max_pairs, int bm, int E_l) {
   return (max_pairs + bm - 1) / bm + (E_l < max_pairs ? E_l : max_pairs);
 }
 
-#ifndef JG_B1_MS
-#define JG_B1_MS 4
-#endif
-#ifndef JG_B1_NS
-#define JG_B1_NS 2
-#endif
-#ifndef JG_B1_WM
-#define JG_B1_WM 2
-#endif
-#ifndef JG_B1_WN
-#define JG_B1_WN 4
-#endif
-#ifndef JG_B1_D
-#define JG_B1_D 3
-#endif
-#ifndef JG_B2_MS
-#define JG_B2_MS 2
-#endif
-#ifndef JG_B2_NS
-#define JG_B2_NS 4
-#endif
-#ifndef JG_B2_WM
-#define JG_B2_WM 4
-#endif
-#ifndef JG_B2_WN
-#define JG_B2_WN 2
-#endif
-#ifndef JG_B2_D
-#define JG_B2_D 3
-#endif
+constexpr int kB1Ms = 4;
+constexpr int kB1Ns = 2;
+constexpr int kB1Wm = 2;
+constexpr int kB1Wn = 4;
+constexpr int kB1D = 3;
+constexpr int kB2Ms = 2;
+constexpr int kB2Ns = 4;
+constexpr int kB2Wm = 4;
+constexpr int kB2Wn = 2;
+constexpr int kB2D = 3;
 
 hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                             const float* s13, const int32_t* counts, const int32_t* offsets,
                             const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                             int max_pairs, hipStream_t stream) {
-  constexpr int BN = 16 * JG_B1_NS * JG_B1_WN;
-  if (I % BN != 0 || H / kBlock < JG_B1_D - 1 || (int64_t)T * H >= kOutOfRange)
+  constexpr int BN = 16 * kB1Ns * kB1Wn;
+  if (I % BN != 0 || H / kBlock < kB1D - 1 || (int64_t)T * H >= kOutOfRange)
     return hipErrorNotSupported;
-  const int grid = big_grid(big_tiles(max_pairs, 16 * JG_B1_MS * JG_B1_WM, E_l) * (I / BN));
-  gemm1_big_kernel<JG_B1_MS, JG_B1_NS, JG_B1_D, JG_B1_WM, JG_B1_WN><<<grid, (JG_B1_WM * JG_B1_WN + 1) * kWave, 0, stream>>>(
-      hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs);
+  const int grid = big_grid(big_tiles(max_pairs, 16 * kB1Ms * kB1Wm, E_l) * (I / BN));
+  gemm1_big_kernel<kB1Ms, kB1Ns, kB1D, kB1Wm, kB1Wn><<<grid, (kB1Wm * kB1Wn + 1) * kWave, 0, stream>>>(
+      hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs,
+      kSchedGemm1);
   return hipGetLastError();
 }
 
@@ -800,11 +812,11 @@ hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s
                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
                             Gemm2Out dst, int H, int I, int E_l, int max_pairs,
                             hipStream_t stream) {
-  constexpr int BN = 16 * JG_B2_NS * JG_B2_WN;
-  if (H % BN != 0 || I / kBlock < JG_B2_D - 1) return hipErrorNotSupported;
-  const int grid = big_grid(big_tiles(max_pairs, 16 * JG_B2_MS * JG_B2_WM, E_l) * (H / BN));
-  gemm2_big_kernel<JG_B2_MS, JG_B2_NS, JG_B2_D, JG_B2_WM, JG_B2_WN><<<grid, (JG_B2_WM * JG_B2_WN + 1) * kWave, 0, stream>>>(
-      C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs);
+  constexpr int BN = 16 * kB2Ns * kB2Wn;
+  if (H % BN != 0 || I / kBlock < kB2D - 1) return hipErrorNotSupported;
+  const int grid = big_grid(big_tiles(max_pairs, 16 * kB2Ms * kB2Wm, E_l) * (H / BN));
+  gemm2_big_kernel<kB2Ms, kB2Ns, kB2D, kB2Wm, kB2Wn><<<grid, (kB2Wm * kB2Wn + 1) * kWave, 0, stream>>>(
+      C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs, kSchedGemm2);
   return hipGetLastError();
 }
 

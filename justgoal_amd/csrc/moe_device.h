@@ -149,15 +149,12 @@ __device__ __forceinline__ void lds_wait(v4u& x, v4u& y, v4u& z, v4u& w) {
 // Weight K-block image in LDS: 16 rows x 128 bytes, row n's 16-byte chunk c stored at position
 // c ^ wblk_swz(n). A DMA instruction h (h = 0, 1) fills rows 8h..8h+7 with whole lines; the MFMA
 // operand read (lane = row n | group g, chunks 2g and 2g+1) is bank-conflict free.
-#ifndef JG_WBLK_SWZ
-#define JG_WBLK_SWZ 0
-#endif
 // 16-byte chunk permutation of row n of a 16-row block (depends on n mod 16 only, so DMA code may
 // pass a tile-level row). ds_read_b128 of the MFMA fragments (lane l reads row l&15, chunks
 // 2(l>>4) and 2(l>>4)+1) measured conflict-free with (n & 7) ^ ((n >> 3) & 1) and 2-way
 // conflicted with (n >> 1) & 7 or n & 7 (the hardware serves a b128 read in 16-lane groups).
 __device__ __forceinline__ int wblk_swz(int row) {
-  return JG_WBLK_SWZ ? ((row >> 1) & 7) : ((row & 7) ^ ((row >> 3) & 1));
+  return (row & 7) ^ ((row >> 3) & 1);
 }
 // Global byte offset, relative to row 0 of the block, that lane `lane` of DMA instruction h
 // fetches; `row_bytes` is the weight row pitch.

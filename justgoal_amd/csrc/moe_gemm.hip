@@ -71,32 +71,20 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 // tiles cheap; the LDS-tiled GEMM2 lost to them everywhere). The streaming kernels' 16-row
 // items re-stream an expert's weights once per 16 rows, so they only win while segments are
 // that short.
-#ifndef JG_STREAM_MAX_ROWS
-#define JG_STREAM_MAX_ROWS 4
-#endif
-#ifndef JG_BIG_ROWS
-#define JG_BIG_ROWS 64
-#endif
-#ifndef JG_G2_STREAM_MAX_ROWS
-#define JG_G2_STREAM_MAX_ROWS 3
-#endif
-#ifndef JG_G2_BIG_ROWS
-#define JG_G2_BIG_ROWS 4
-#endif
+constexpr int kStreamMaxRows = 4;
+constexpr int kBigRows = 64;
+constexpr int kG2StreamMaxRows = 3;
+constexpr int kG2BigRows = 4;
 
-#ifndef JG_TILE_MT8_ROWS
-#define JG_TILE_MT8_ROWS 256
-#endif
+constexpr int kTileMt8Rows = 256;
 
 // M sub-tiles (of 16 rows) per work item for an expected segment length.
 static inline int stream_mt(int rows_hint) { return rows_hint <= 16 ? 1 : rows_hint <= 32 ? 2 : 4; }
 // LDS-tiled GEMM1 tile height: 32 rows up to 16 expected rows per expert (T=256: 122.8 ->
 // 116.7 us), 64 above (128-row tiles measured far slower at 32: 239 vs 158 us).
-#ifndef JG_TILE_MT2_ROWS
-#define JG_TILE_MT2_ROWS 16
-#endif
+constexpr int kTileMt2Rows = 16;
 static inline int tile_mt(int rows_hint) {
-  return rows_hint <= JG_TILE_MT2_ROWS ? 2 : rows_hint <= JG_TILE_MT8_ROWS ? 4 : 8;
+  return rows_hint <= kTileMt2Rows ? 2 : rows_hint <= kTileMt8Rows ? 4 : 8;
 }
 
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
@@ -104,10 +92,10 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t*
                         const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                         int max_pairs, int rows_hint, hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= JG_STREAM_MAX_ROWS)
+  if (rows_hint <= kStreamMaxRows)
     return launch_gemm1_stream(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I,
                                E_l, max_pairs, stream_mt(rows_hint), stream);
-  if (rows_hint >= JG_BIG_ROWS) {
+  if (rows_hint >= kBigRows) {
     const hipError_t b = launch_gemm1_big(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C,
                                           T, H, I, E_l, max_pairs, stream);
     if (b != hipErrorNotSupported) return b;
@@ -124,10 +112,10 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
                         Gemm2Out dst, int H, int I, int E_l, int max_pairs, int rows_hint,
                         hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= JG_G2_STREAM_MAX_ROWS)
+  if (rows_hint <= kG2StreamMaxRows)
     return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
                                max_pairs, stream_mt(rows_hint), stream);
-  if (rows_hint >= JG_G2_BIG_ROWS) {
+  if (rows_hint >= kG2BigRows) {
     const hipError_t b = launch_gemm2_big(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
                                           max_pairs, stream);
     if (b != hipErrorNotSupported) return b;

@@ -442,12 +442,8 @@ static inline int ring_depth(int nkb, int dmax) {
   return d;
 }
 
-#ifndef JG_G1_STREAM_D
-#define JG_G1_STREAM_D 8
-#endif
-#ifndef JG_G2_STREAM_D
-#define JG_G2_STREAM_D 8
-#endif
+constexpr int kG1StreamD = 8;
+constexpr int kG2StreamD = 8;
 
 hipError_t launch_gemm1_stream(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                                const float* s13, const int32_t* counts, const int32_t* offsets,
@@ -463,7 +459,7 @@ hipError_t launch_gemm1_stream(const uint8_t* hs, const float* hs_scale, const u
         hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l);                 \
     return hipGetLastError();                                                                  \
   }
-  const int d = ring_depth(nkb, mt == 1 ? JG_G1_STREAM_D : 4);
+  const int d = ring_depth(nkb, mt == 1 ? kG1StreamD : 4);
   if (mt == 1) {
     if (d >= 8) JG_G1S(1, 8)
     if (d == 4) JG_G1S(1, 4)
@@ -495,7 +491,7 @@ hipError_t launch_gemm2_stream(const uint16_t* C, const uint8_t* w2, const float
         C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs);                  \
     return hipGetLastError();                                                                  \
   }
-  const int d = ring_depth(nkb, mt == 1 ? JG_G2_STREAM_D : mt == 2 ? 4 : 2);
+  const int d = ring_depth(nkb, mt == 1 ? kG2StreamD : mt == 2 ? 4 : 2);
   if (mt == 1) {
     if (d >= 8) JG_G2S(1, 8)
     if (d == 4) JG_G2S(1, 4)

@@ -285,9 +285,7 @@ static inline long long tile_count(int max_pairs, int bm, int E_l) {
 
 // Ring depths (lead D-1 blocks). D = 3 keeps two workgroups per CU within the 160 KiB of LDS,
 // which measured faster than deeper rings at one workgroup per CU.
-#ifndef JG_G1T_D
-#define JG_G1T_D 3
-#endif
+constexpr int kG1tD = 3;
 
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                              const float* s13, const int32_t* counts, const int32_t* offsets,
@@ -304,9 +302,9 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
         hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs);       \
     return hipGetLastError();                                                                   \
   }
-  if (mt <= 2) JG_G1T(2, JG_G1T_D)
-  if (mt <= 4) JG_G1T(4, JG_G1T_D)
-  JG_G1T(8, (JG_G1T_D > 4 ? 4 : JG_G1T_D))  // a 128-row tile leaves room for 4 slots
+  if (mt <= 2) JG_G1T(2, kG1tD)
+  if (mt <= 4) JG_G1T(4, kG1tD)
+  JG_G1T(8, (kG1tD > 4 ? 4 : kG1tD))  // a 128-row tile leaves room for 4 slots
 #undef JG_G1T
 }
 

@@ -72,52 +72,77 @@ def _check_shapes(geom: Geometry, T, logits, hs, hs_scale, w13, s13, w2, s2):
             raise ValueError(f"{name}: expected shape {shape}, got {tuple(t.shape)}")
 
 
+def _routing_args(geom: Geometry, routing_logits, routing_bias, on_gpu=True):
+    """Coerced logits fp32 [T, E] and bias bf16 [E] (or None), shape-checked."""
+    if routing_logits.dim() != 2 or int(routing_logits.shape[1]) != geom.num_experts:
+        raise ValueError(f"routing_logits: expected shape (T, {geom.num_experts}), got "
+                         f"{tuple(routing_logits.shape)}")
+    if routing_logits.dtype != torch.float32 or not routing_logits.is_contiguous():
+        routing_logits = routing_logits.contiguous().to(torch.float32)
+    if routing_bias is not None:
+        if tuple(routing_bias.shape) != (geom.num_experts,):
+            raise ValueError(f"routing_bias: expected shape ({geom.num_experts},), got "
+                             f"{tuple(routing_bias.shape)}")
+        if routing_bias.dtype != torch.bfloat16 or not routing_bias.is_contiguous():
+            routing_bias = routing_bias.contiguous().to(torch.bfloat16)
+        if routing_bias.device != routing_logits.device:
+            raise ValueError("routing_bias must be on the logits' device")
+    if on_gpu and routing_logits.device.type != "cuda":
+        raise ValueError("routing_logits must be on a GPU")
+    return routing_logits, routing_bias
+
+
+def _prepare(geom: Geometry, routing_logits, routing_bias, hidden_states, hidden_states_scale,
+             gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output):
+    """The argument rules of ``run`` (t1/main.py:99-133 coercions plus shape, dtype, contiguity
+    and device checks), shared by ``run`` and ``bind``. Returns (T, device, tensors, bias,
+    output) with ``tensors`` = (logits, hs, hs_scale, w13, s13, w2, s2)."""
+    T = int(routing_logits.shape[0])
+    dev = hidden_states.device
+    routing_logits, routing_bias = _routing_args(geom, routing_logits, routing_bias, on_gpu=False)
+    for name, t in (("hidden_states", hidden_states), ("gemm1_weights", gemm1_weights),
+                    ("gemm2_weights", gemm2_weights)):
+        if t.dtype != F8 or not t.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous float8_e4m3fn tensor")
+    hss = hidden_states_scale.contiguous().to(torch.float32)
+    s13 = gemm1_weights_scale.contiguous().to(torch.float32)
+    s2 = gemm2_weights_scale.contiguous().to(torch.float32)
+    _check_shapes(geom, T, routing_logits, hidden_states, hss, gemm1_weights, s13, gemm2_weights,
+                  s2)
+    if output is None:
+        output = torch.empty((T, geom.hidden), dtype=torch.bfloat16, device=dev)
+    elif (output.dtype != torch.bfloat16 or tuple(output.shape) != (T, geom.hidden)
+          or not output.is_contiguous()):
+        raise ValueError("output must be a contiguous bf16 [T, H] tensor")
+    tensors = (routing_logits, hidden_states, hss, gemm1_weights, s13, gemm2_weights, s2)
+    devs = [t.device for t in tensors] + [output.device]
+    if routing_bias is not None:
+        devs.append(routing_bias.device)
+    if any(d != dev for d in devs) or dev.type != "cuda":
+        raise ValueError("all tensors must be on the same GPU")
+    return T, dev, tensors, routing_bias, output
+
+
 @torch.no_grad()
 def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
         gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
         routed_scaling_factor, output=None, *, geometry: Geometry = DS_V3):
     """FP8 block-scale MoE forward. Returns ``output`` (allocated when not given)."""
     geom = geometry
-    T = int(routing_logits.shape[0])
-    dev = hidden_states.device
     off = _scalar(local_expert_offset, int)
     rsf = _scalar(routed_scaling_factor, float)
-    if routing_logits.dtype != torch.float32 or not routing_logits.is_contiguous():
-        routing_logits = routing_logits.contiguous().to(torch.float32)
-    if routing_bias is not None and (routing_bias.dtype != torch.bfloat16
-                                     or not routing_bias.is_contiguous()):
-        routing_bias = routing_bias.contiguous().to(torch.bfloat16)
-    for name, t in (("hidden_states", hidden_states), ("gemm1_weights", gemm1_weights),
-                    ("gemm2_weights", gemm2_weights)):
-        if t.dtype != F8 or not t.is_contiguous():
-            raise TypeError(f"{name} must be a contiguous float8_e4m3fn tensor")
-    hidden_states_scale = hidden_states_scale.contiguous().to(torch.float32)
-    gemm1_weights_scale = gemm1_weights_scale.contiguous().to(torch.float32)
-    gemm2_weights_scale = gemm2_weights_scale.contiguous().to(torch.float32)
-    _check_shapes(geom, T, routing_logits, hidden_states, hidden_states_scale, gemm1_weights,
-                  gemm1_weights_scale, gemm2_weights, gemm2_weights_scale)
-    if routing_bias is not None and tuple(routing_bias.shape) != (geom.num_experts,):
-        raise ValueError(f"routing_bias: expected shape ({geom.num_experts},)")
-    if output is None:
-        output = torch.empty((T, geom.hidden), dtype=torch.bfloat16, device=dev)
-    elif (output.dtype != torch.bfloat16 or tuple(output.shape) != (T, geom.hidden)
-          or not output.is_contiguous()):
-        raise ValueError("output must be a contiguous bf16 [T, H] tensor")
+    T, dev, tensors, bias, output = _prepare(
+        geom, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+        gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
     if T == 0:
         return output
-    tensors = (routing_logits, hidden_states, hidden_states_scale, gemm1_weights,
-               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
-    if any(t.device != dev for t in tensors) or dev.type != "cuda":
-        raise ValueError("all tensors must be on the same GPU")
     ws = workspace(geom, T, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     g = geom.c_struct()
-    bias_ptr = None if routing_bias is None else routing_bias.data_ptr()
+    bias_ptr = None if bias is None else bias.data_ptr()
     rc = _lib.lib().moe_run_ex(
-        ctypes.byref(g), routing_logits.data_ptr(), bias_ptr, hidden_states.data_ptr(),
-        hidden_states_scale.data_ptr(), gemm1_weights.data_ptr(), gemm1_weights_scale.data_ptr(),
-        gemm2_weights.data_ptr(), gemm2_weights_scale.data_ptr(), off, rsf, output.data_ptr(),
-        ws.data_ptr(), T, stream)
+        ctypes.byref(g), tensors[0].data_ptr(), bias_ptr, *[t.data_ptr() for t in tensors[1:]],
+        off, rsf, output.data_ptr(), ws.data_ptr(), T, stream)
     _lib.check(rc, "moe_run_ex")
     return output
 
@@ -149,29 +174,15 @@ class BoundCall:
 def bind(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
          gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
          routed_scaling_factor, output=None, *, geometry: Geometry = DS_V3) -> BoundCall:
-    """Validate once (same rules as ``run``) and return a ``BoundCall``."""
+    """Validate once (the same rules as ``run``) and return a ``BoundCall``."""
     geom = geometry
-    T = int(routing_logits.shape[0])
-    dev = hidden_states.device
-    routing_logits = routing_logits.contiguous().to(torch.float32)
-    if routing_bias is not None:
-        routing_bias = routing_bias.contiguous().to(torch.bfloat16)
-    for name, t in (("hidden_states", hidden_states), ("gemm1_weights", gemm1_weights),
-                    ("gemm2_weights", gemm2_weights)):
-        if t.dtype != F8 or not t.is_contiguous():
-            raise TypeError(f"{name} must be a contiguous float8_e4m3fn tensor")
-    hss = hidden_states_scale.contiguous().to(torch.float32)
-    s13 = gemm1_weights_scale.contiguous().to(torch.float32)
-    s2 = gemm2_weights_scale.contiguous().to(torch.float32)
-    _check_shapes(geom, T, routing_logits, hidden_states, hss, gemm1_weights, s13, gemm2_weights,
-                  s2)
-    if output is None:
-        output = torch.empty((T, geom.hidden), dtype=torch.bfloat16, device=dev)
-    tensors = (routing_logits, hidden_states, hss, gemm1_weights, s13, gemm2_weights, s2)
+    T, dev, tensors, bias, output = _prepare(
+        geom, routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+        gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
     # a bound call owns its workspace, so bound calls on different streams never share one
     ws = torch.empty(max(_lib.workspace_layout(geom, T)["total"], 1), dtype=torch.uint8,
                      device=dev)
-    return BoundCall(geom, tensors, routing_bias, _scalar(local_expert_offset, int),
+    return BoundCall(geom, tensors, bias, _scalar(local_expert_offset, int),
                      _scalar(routed_scaling_factor, float), output, ws, T)
 
 
@@ -181,10 +192,8 @@ def route(routing_logits, routing_bias, local_expert_offset, routed_scaling_fact
     """Routing + permute only; returns views of the workspace regions they write."""
     geom = geometry
     T = int(routing_logits.shape[0])
+    routing_logits, routing_bias = _routing_args(geom, routing_logits, routing_bias)
     dev = routing_logits.device
-    routing_logits = routing_logits.contiguous().to(torch.float32)
-    if routing_bias is not None:
-        routing_bias = routing_bias.contiguous().to(torch.bfloat16)
     ws = workspace(geom, T, dev)
     g = geom.c_struct()
     rc = _lib.lib().moe_route_ex(

@@ -152,3 +152,59 @@ def test_error_strings():
     for rc, word in ((-1, "argument"), (-2, "geometry"), (-3, "gfx950")):
         assert word in L.moe_error_string(rc).decode()
     assert L.moe_error_string(-99).decode() == "unknown error"
+
+
+def _cpu_args(geom, T, **over):
+    """Operator arguments of the right shapes and dtypes on the CPU (host-side checks only)."""
+    import torch
+    H, I, E, El = geom.hidden, geom.intermediate, geom.num_experts, geom.local_experts
+    f8 = torch.float8_e4m3fn
+    d = dict(routing_logits=torch.zeros(T, E), routing_bias=torch.zeros(E, dtype=torch.bfloat16),
+             hidden_states=torch.zeros(T, H, dtype=f8), hidden_states_scale=torch.ones(H // 128, T),
+             gemm1_weights=torch.zeros(El, 2 * I, H, dtype=f8),
+             gemm1_weights_scale=torch.ones(El, 2 * I // 128, H // 128),
+             gemm2_weights=torch.zeros(El, H, I, dtype=f8),
+             gemm2_weights_scale=torch.ones(El, H // 128, I // 128),
+             local_expert_offset=0, routed_scaling_factor=2.5)
+    d.update(over)
+    return d
+
+
+MINI = Geometry(256, 128, 64, 16, 4, 4, 2, ROUTING_DS, "mini")
+
+
+@pytest.mark.parametrize("entry", ["run", "bind"])
+@pytest.mark.parametrize("bad", ["output_shape", "output_dtype", "bias_len", "logits_width",
+                                 "hs_rows", "scale_layout", "cpu_tensors"])
+def test_wrappers_reject_bad_arguments_before_any_launch(entry, bad):
+    """run() and bind() share one set of argument checks: a wrong-sized or misplaced tensor is a
+    ValueError / TypeError on the host, never a kernel reading or writing out of bounds."""
+    import torch
+    from justgoal_amd import moe
+    T = 5
+    over = {}
+    if bad == "output_shape":
+        over["output"] = torch.empty(T + 1, MINI.hidden, dtype=torch.bfloat16)
+    elif bad == "output_dtype":
+        over["output"] = torch.empty(T, MINI.hidden, dtype=torch.float32)
+    elif bad == "bias_len":
+        over["routing_bias"] = torch.zeros(MINI.num_experts + 1, dtype=torch.bfloat16)
+    elif bad == "logits_width":
+        over["routing_logits"] = torch.zeros(T, MINI.num_experts - 64)
+    elif bad == "hs_rows":
+        over["hidden_states"] = torch.zeros(T + 2, MINI.hidden, dtype=torch.float8_e4m3fn)
+    elif bad == "scale_layout":
+        over["hidden_states_scale"] = torch.ones(T, MINI.hidden // 128)  # not transposed
+    kw = _cpu_args(MINI, T, **over)
+    with pytest.raises((ValueError, TypeError)):
+        getattr(moe, entry)(**kw, geometry=MINI)
+
+
+@pytest.mark.parametrize("bad", ["bias_len", "logits_width"])
+def test_route_rejects_bad_shapes(bad):
+    import torch
+    from justgoal_amd import moe
+    lg = torch.zeros(3, MINI.num_experts - (64 if bad == "logits_width" else 0))
+    b = torch.zeros(MINI.num_experts + (1 if bad == "bias_len" else 0), dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        moe.route(lg, b, 0, 2.5, geometry=MINI)

@@ -54,9 +54,9 @@ def test_routing_stats_read_the_given_workspace():
 def test_kernel_family_thresholds_match_the_library_source():
     import re
     src = open(os.path.join(ROOT, "justgoal_amd", "csrc", "moe_gemm.hip")).read()
-    stream = int(re.search(r"#define JG_STREAM_MAX_ROWS (\d+)", src).group(1))
-    big = int(re.search(r"#define JG_BIG_ROWS (\d+)", src).group(1))
-    g2 = int(re.search(r"#define JG_G2_STREAM_MAX_ROWS (\d+)", src).group(1))
+    stream = int(re.search(r"constexpr int kStreamMaxRows = (\d+);", src).group(1))
+    big = int(re.search(r"constexpr int kBigRows = (\d+);", src).group(1))
+    g2 = int(re.search(r"constexpr int kG2StreamMaxRows = (\d+);", src).group(1))
     assert (bench.GEMM1_STREAM_MAX_ROWS, bench.GEMM1_BIG_ROWS) == (stream, big)
     assert bench.GEMM2_STREAM_MAX_ROWS == g2
     from justgoal_amd import inputs as jin
