@@ -540,3 +540,41 @@ def test_graph_replay_matches_eager(gpu, T):
         assert torch.equal(got, ref), f"replay with seed {seed} differs from the eager call"
     del g
     release_workspaces()
+
+
+def _extreme_logits(T, E, seed):
+    """Logits spread over every binade of |x| from 2^-30 to 120 (both signs), with runs of
+    values around the sigmoid's special points (0, -87, the fp32 exp limits) and a few huge or
+    subnormal ones, so the fp32 sigmoid/exp of the kernel is compared with the oracle's on its
+    range reduction, its two-float correction, the e^x branch below -87 and the clamps."""
+    g = torch.Generator().manual_seed(seed)
+    mag = torch.exp2(torch.rand(T, E, generator=g) * (np.log2(120.0) + 30.0) - 30.0)
+    sign = torch.where(torch.rand(T, E, generator=g) < 0.5, -1.0, 1.0)
+    x = mag * sign
+    special = torch.tensor([0.0, -0.0, -87.0, -86.99999, -87.00001, -88.72, -103.0, -104.0,
+                            -200.0, 88.0, 104.0, 1e30, -1e30, 1e-40, -1e-40, 15.9, -15.9])
+    rows = torch.randint(0, T, (T // 2,), generator=g)
+    cols = torch.randint(0, E, (T // 2,), generator=g)
+    x[rows, cols] = special[torch.arange(T // 2) % len(special)]
+    # tokens whose every sigmoid is subnormal (x in [-103, -88]): the selected weights
+    # then come from subnormal sigmoids and a denominator dominated by the 1e-20 guard
+    x[:16] = -88.0 - 15.0 * torch.rand(16, E, generator=g)
+    return x.float()
+
+
+@pytest.mark.parametrize("geom", [DS_V3, QWEN3, MINI_DS])
+def test_route_extreme_logits_bit_exact(gpu, geom):
+    """Routing of logits far outside N(0,1): indices and weights bit-identical to the oracle,
+    whose fp32 sigmoid is pinned against the correctly rounded one on every binade."""
+    from justgoal_amd.moe import route
+    say(f"extreme logits: {geom.name}")
+    T = 2048
+    lg = _extreme_logits(T, geom.num_experts, seed=11)
+    b = (torch.randn(geom.num_experts, generator=torch.Generator().manual_seed(3)) * 0.1).to(
+        torch.bfloat16)
+    rsf = 2.5 if geom.routing_method == ROUTING_DS else 1.0
+    v = route(lg.to(gpu), b.to(gpu), 0, rsf, geometry=geom)
+    torch.cuda.synchronize()
+    idx, w = oracle.route(lg, b, geom, rsf)
+    np.testing.assert_array_equal(v["topk_idx"].cpu().numpy(), idx)
+    np.testing.assert_array_equal(v["topk_w"].cpu().numpy().view(np.uint32), w.view(np.uint32))
