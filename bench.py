@@ -8,7 +8,8 @@ run: the T=16 plumbing case, the decode-sized T=64 headline, the prefill-sized T
 skewed T=16384 case and the Qwen3-style T=1024 case. Each workload first runs W warm-up calls and
 then keeps calling for at least ``--settle-ms`` of wall time (clocks settle over tens of ms of
 load, whatever the call length), then times K (at least 20) back-to-back calls between two HIP
-events.
+events. Consecutive calls cycle through ``--weight-sets`` (default 3) distinct weight sets, as
+consecutive MoE layers would, so no call finds the previous call's weights in a cache.
 
 Prints ONE JSON line. ``value`` is TFLOP/s of the headline workload over algorithmic FLOPs
 (6*H*I per local (token, expert) pair, pairs counted from the routing of the run). Each workload
@@ -150,18 +151,32 @@ def roofline_block(stage, kernel, ms, flops, nbytes, peak_tflops, workload):
             "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "avg_launch_ms": ms}
 
 
-def measure(cfg, weights_dev, steps, warmup, settle_ms, dev, seed=None):
+def measure(cfg, weight_sets, steps, warmup, settle_ms, dev, seed=None):
+    """Times one workload. With several weight sets (distinct layers' weights), consecutive
+    calls cycle through them, so no call finds the previous call's weights in a cache."""
     geom = cfg.geom
     seed = cfg.seed if seed is None else seed
     act = jin.make_activations(geom, cfg.tokens, seed=seed, device=dev,
                                skew_experts=cfg.skew_experts, skew_offset=cfg.skew_offset)
-    w13, s13, w2, s2 = weights_dev
-    kw = dict(act, gemm1_weights=w13, gemm1_weights_scale=s13, gemm2_weights=w2,
-              gemm2_weights_scale=s2, local_expert_offset=0,
-              routed_scaling_factor=2.5 if geom.routing_method == 0 else 1.0)
-    call = bind(**kw, geometry=geom)
-    ms, n_warm = settle_and_time(call, steps, warmup, settle_ms, dev)
-    st = stage_times(call, min(steps, 20), dev)
+    calls = []
+    for w13, s13, w2, s2 in weight_sets:
+        kw = dict(act, gemm1_weights=w13, gemm1_weights_scale=s13, gemm2_weights=w2,
+                  gemm2_weights_scale=s2, local_expert_offset=0,
+                  routed_scaling_factor=2.5 if geom.routing_method == 0 else 1.0)
+        calls.append(bind(**kw, geometry=geom))
+    kw = dict(kw, gemm1_weights=weight_sets[0][0], gemm1_weights_scale=weight_sets[0][1],
+              gemm2_weights=weight_sets[0][2], gemm2_weights_scale=weight_sets[0][3])
+    call = calls[0]
+    if len(calls) == 1:
+        timed = call
+    else:
+        state = [0]
+
+        def timed():
+            state[0] = (state[0] + 1) % len(calls)
+            return calls[state[0]]()
+    ms, n_warm = settle_and_time(timed, steps, warmup, settle_ms, dev)
+    st = stage_times(timed, min(steps, 20), dev)
     pairs, active, tok_local = routing_stats(geom, cfg.tokens, call.workspace)
     if pairs == 0:
         raise RuntimeError(f"{cfg.name}: no routed pairs read back from the call's workspace")
@@ -175,7 +190,8 @@ def measure(cfg, weights_dev, steps, warmup, settle_ms, dev, seed=None):
     g2 = roofline_block("gemm2", gemm2_kernel_name(cfg), st["gemm2"], g2_flops, g2_bytes,
                         PEAK_BF16_TFLOPS, cfg.name)
     res = dict(workload=cfg.name, geometry=geom.name, tokens=cfg.tokens, seed=seed,
-               ms_per_call=ms, steps=steps, warmup_calls=n_warm, tflops=tflops, gb_s=gbs,
+               ms_per_call=ms, steps=steps, warmup_calls=n_warm, weight_sets=len(calls),
+               tflops=tflops, gb_s=gbs,
                pairs=pairs, active_experts=active, algorithmic_flops=flops,
                algorithmic_bytes=bytes_, call_floor_ms=t_floor_ms,
                call_floor_frac=t_floor_ms / ms, hbm_frac=gbs / PEAK_HBM_GBS,
@@ -261,6 +277,10 @@ def main():
                     help="headline workload (value, ms_per_step)")
     ap.add_argument("--workloads", default=",".join(DEFAULT_WORKLOADS),
                     help="comma-separated workloads to measure (the headline is always included)")
+    ap.add_argument("--weight-sets", type=int, default=3,
+                    help="distinct weight sets that consecutive calls cycle through (consecutive "
+                         "MoE layers have different weights; with 1 set, repeated calls of a "
+                         "small batch partly hit the previous call's weights in the 256 MB MALL)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quant", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -296,7 +316,8 @@ def main():
     for geom in dict.fromkeys(jin.CONFIGS[n].geom for n in names):
         t0 = time.time()
         log(f"[bench] generating {geom.name} weights")
-        wts = tuple(t.to(dev) for t in jin.make_weights(geom, seed=0))
+        wts = [tuple(t.to(dev) for t in jin.make_weights(geom, seed=k))
+               for k in range(args.weight_sets)]
         log(f"[bench] weights ready in {time.time() - t0:.1f}s")
         for n in names:
             cfg = jin.CONFIGS[n]
@@ -335,14 +356,15 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8-e4m3 (GEMM1) / bf16 (GEMM2), fp32 accumulate",
         "data": f"synthetic (seed {head_cfg.seed}: N(0,1) activations/logits, N(0,0.1) bias, "
-                "N(0,0.02) weights, 128x128 block scales)",
+                f"N(0,0.02) weights, 128x128 block scales; {args.weight_sets} weight sets "
+                "cycled call to call)",
         "config": {"workload": head_cfg.name, "geometry": head_cfg.geom.name,
                    "tokens": head_cfg.tokens, "seed": head_cfg.seed,
                    "local_pairs": head["pairs"], "active_local_experts": head["active_experts"],
                    "hidden": head_cfg.geom.hidden, "intermediate": head_cfg.geom.intermediate,
                    "local_experts": head_cfg.geom.local_experts, "top_k": head_cfg.geom.top_k,
                    "parallelism": "single GPU (EP rank 0 of 8: local experts 0..31)",
-                   "settle_ms": args.settle_ms},
+                   "settle_ms": args.settle_ms, "weight_sets": args.weight_sets},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "headline": head,

@@ -98,6 +98,30 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds_base, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_base, 16, voff, soff, 0, 0);
 }
 
+// 16-byte global load with the non-temporal hint, for data a kernel reads exactly once.
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  typedef unsigned v4_t __attribute__((ext_vector_type(4)));
+  const v4_t v = __builtin_nontemporal_load((const v4_t*)p);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+// Cache-policy bit of gfx950 vector memory instructions marking a non-temporal (streaming)
+// access.
+constexpr int kCachePolicyNT = 2;
+
+// dma16 for data this launch reads exactly once (the weight stream of the kernels that see each
+// weight byte once per call): the non-temporal hint keeps those lines from displacing reused
+// ones (activation rows, C fragments). Measured on the weight-streaming and LDS-tiled kernels,
+// with three weight sets in rotation so no call finds its weights cached: DS-V3 T=64 call
+// 146.9 -> 134.5 us, T=256 203.9 -> 188.6 us, Qwen3-style T=128 499.6 -> 474.4 us. The large-tile
+// kernels, which reuse each weight tile across M-tiles through L2, got slower with it
+// (T=4096 GEMM1 217 -> 238 us) and keep the default policy.
+__device__ __forceinline__ void dma16_stream(__amdgpu_buffer_rsrc_t r, void* lds_base,
+                                             uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_base, 16, voff, soff, 0,
+                                           kCachePolicyNT);
+}
+
 // 4 bytes per lane (e.g. one scale per row) into LDS at lds_base + 4 * lane.
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff,
                                      uint32_t soff) {

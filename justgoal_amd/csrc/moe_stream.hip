@@ -142,10 +142,10 @@ __global__ __launch_bounds__(256) void gemm1_stream_kernel(
     const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
     const uint32_t w0 = dead ? kNoFetch : dma0, w1 = dead ? kNoFetch : dma1;
     uint8_t* slot = my_ring + d * 2 * kWBlk;
-    dma16(wres, slot, w0, ws);
-    dma16(wres, slot + 1024, w1, ws);
-    dma16(wres, slot + kWBlk, w0, ws + (uint32_t)I * H);
-    dma16(wres, slot + kWBlk + 1024, w1, ws + (uint32_t)I * H);
+    dma16_stream(wres, slot, w0, ws);
+    dma16_stream(wres, slot + 1024, w1, ws);
+    dma16_stream(wres, slot + kWBlk, w0, ws + (uint32_t)I * H);
+    dma16_stream(wres, slot + kWBlk + 1024, w1, ws + (uint32_t)I * H);
   };
 
   // Prologue in issue order: the loop's wait counts assume every slot's loads went out
@@ -322,8 +322,8 @@ __global__ __launch_bounds__(256) void gemm2_stream_kernel(
         make_rsrc(uniform(second ? nxt.wbase : cur.wbase), (uint32_t)H * I);
     const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
     uint8_t* slot = my_ring + d * kWBlk;
-    dma16(wres, slot, dead ? kNoFetch : dma0, ws);
-    dma16(wres, slot + 1024, dead ? kNoFetch : dma1, ws);
+    dma16_stream(wres, slot, dead ? kNoFetch : dma0, ws);
+    dma16_stream(wres, slot + 1024, dead ? kNoFetch : dma1, ws);
   };
 
   // Prologue in issue order: the loop's wait counts assume every slot's loads went out

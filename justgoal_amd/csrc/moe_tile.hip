@@ -157,10 +157,10 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
         make_rsrc(uniform(second ? nxt.wbase : cur.wbase), 2u * I * H);
     const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
     uint8_t* b = my_bring + slot * 2 * kWBlk;
-    dma16(wres, b, dma0, ws);
-    dma16(wres, b + 1024, dma1, ws);
-    dma16(wres, b + kWBlk, dma0, ws + (uint32_t)I * H);
-    dma16(wres, b + kWBlk + 1024, dma1, ws + (uint32_t)I * H);
+    dma16_stream(wres, b, dma0, ws);
+    dma16_stream(wres, b + 1024, dma1, ws);
+    dma16_stream(wres, b + kWBlk, dma0, ws + (uint32_t)I * H);
+    dma16_stream(wres, b + kWBlk + 1024, dma1, ws + (uint32_t)I * H);
   };
 
   // Blocks 0..D-2 of the first item; block s+D-1 is issued at step s.
