@@ -105,6 +105,12 @@ __device__ __forceinline__ uint4 load_nt16(const void* p) {
   return uint4{v[0], v[1], v[2], v[3]};
 }
 
+// 16-byte global store with the non-temporal hint, for output nothing in the launch reads back.
+__device__ __forceinline__ void store_nt16(void* p, uint4 v) {
+  typedef unsigned v4_t __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(v4_t{v.x, v.y, v.z, v.w}, (v4_t*)p);
+}
+
 // Cache-policy bit of gfx950 vector memory instructions marking a non-temporal (streaming)
 // access.
 constexpr int kCachePolicyNT = 2;

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
   const int c = c8 * 8;
   uint4* dst = (uint4*)(out + (size_t)t * H + c);
   if (n == 0) {
-    *dst = uint4{0u, 0u, 0u, 0u};
+    store_nt16(dst, uint4{0u, 0u, 0u, 0u});
     return;
   }
   float s[8];
@@ -53,7 +53,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
       s[2 * i + 1] = first ? hi : s[2 * i + 1] + hi;
     }
   };
-  // Every row is read once: non-temporal loads (T=16384 skewed: 216 -> 192 us).
+  // Every row is read once and the output written once: non-temporal loads and stores (T=16384
+  // skewed: 216 -> 192 us with the loads, -> 182 us with the stores too).
   add(load_nt16(dst), true);
   const uint16_t* prow = partial + (size_t)t * (k_local - 1) * H + c;
   for (int j = 0; j + 1 < n; ++j) add(load_nt16(prow + (size_t)j * H), false);
@@ -62,20 +63,22 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
   o.y = (uint32_t)float_to_bf16_bits(s[2]) | ((uint32_t)float_to_bf16_bits(s[3]) << 16);
   o.z = (uint32_t)float_to_bf16_bits(s[4]) | ((uint32_t)float_to_bf16_bits(s[5]) << 16);
   o.w = (uint32_t)float_to_bf16_bits(s[6]) | ((uint32_t)float_to_bf16_bits(s[7]) << 16);
-  *dst = o;
+  store_nt16(dst, o);
 }
 
-// Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from a sweep
-// over T = 64..16384 (DS-V3) and 128..1024 (Qwen3-style): GEMM1 streams weights up to 4
-// expected rows, uses the LDS-tiled kernels up to 63 and the large tiles from 64; GEMM2 streams
-// up to 3 and uses the large tiles above (their padding-row skip keeps part-filled 128-row
-// tiles cheap; the LDS-tiled GEMM2 lost to them everywhere). The streaming kernels' 16-row
-// items re-stream an expert's weights once per 16 rows, so they only win while segments are
-// that short.
-constexpr int kStreamMaxRows = 4;
+// Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from sweeps
+// over DS-V3 T = 16..16384 and Qwen3-style T = 128..1024: GEMM1 streams weights up to 1 expected
+// row, uses the LDS-tiled kernels up to 63 and the large tiles from 64; GEMM2 streams up to 4
+// and uses the large tiles above (their padding-row skip keeps part-filled 128-row tiles cheap;
+// the LDS-tiled GEMM2 lost to them everywhere). The streaming kernels' 16-row items re-stream an
+// expert's weights once per 16 rows, so they only win while segments are that short. With the
+// non-temporal weight stream of the streaming and LDS-tiled kernels, moving GEMM1's switch from
+// 4 to 1 and GEMM2's from 3 to 4 took DS-V3 T=64 from 133.5 to 132.1 us and T=128 from 185.6
+// to 171.3 us (two weight sets in rotation; T=16, 32, 192 and 256 unchanged).
+constexpr int kStreamMaxRows = 1;
 constexpr int kBigRows = 64;
-constexpr int kG2StreamMaxRows = 3;
-constexpr int kG2BigRows = 4;
+constexpr int kG2StreamMaxRows = 4;
+constexpr int kG2BigRows = 5;
 
 constexpr int kTileMt8Rows = 256;
 

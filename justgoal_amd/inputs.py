@@ -50,7 +50,9 @@ CONFIGS = {
     "qwen3_t128": Config("qwen3_t128", QWEN3, 128, seed=BENCH_SEED),
     "qwen3_t512": Config("qwen3_t512", QWEN3, 512, seed=BENCH_SEED),
     # prefill chunks between the decode and the large-batch cases (LDS-tile kernels)
+    "ds_t32": Config("ds_t32", DS_V3, 32, seed=BENCH_SEED),
     "ds_t128": Config("ds_t128", DS_V3, 128, seed=BENCH_SEED),
+    "ds_t192": Config("ds_t192", DS_V3, 192, seed=BENCH_SEED),
     "ds_t256": Config("ds_t256", DS_V3, 256, seed=BENCH_SEED),
     "ds_t512": Config("ds_t512", DS_V3, 512, seed=BENCH_SEED),
     "ds_t768": Config("ds_t768", DS_V3, 768, seed=BENCH_SEED),

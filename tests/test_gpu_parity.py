@@ -259,7 +259,8 @@ def test_definition_token_counts_via_reference_binding(gpu, T):
 
 
 # Qwen3 geometry (H=4096, I=1536: 12 K blocks in GEMM2) across the kernel families:
-# T * top_k / E = 0.06 and 0.5 stream weights, 4 and ~19 use the LDS-tiled GEMM1.
+# T * top_k / E = 0.06 and 0.5 stream weights in both GEMMs, 4 uses the LDS-tiled GEMM1 and the
+# streaming GEMM2, ~19 the LDS-tiled GEMM1 and the large-tile GEMM2.
 @pytest.mark.parametrize("T", [1, 8, 64, 300])
 def test_qwen3_small_and_mid_batches(gpu, T):
     say(f"qwen3 T={T}")
@@ -361,11 +362,25 @@ def boundary_counts(T, E=64, top_k=8):
 @pytest.mark.parametrize("T", [128, 256, 512, 1024])
 def test_segment_length_boundaries(gpu, T):
     """Expert segments of exactly 1, 15, 16, 17, 31, 32, 33, ... pairs (and empty experts): the
-    tile edges of the streaming (T=128), LDS-tile (T=256) and large-tile (T=512, 1024) kernels,
+    tile edges of the LDS-tile (T=128, 256) and large-tile (T=512, 1024) kernels,
     including large-tile waves whose rows of a tile are all padding."""
     counts = boundary_counts(T)
     lg = logits_for_counts(counts, T, SEG_GEOM.num_experts)
     _, ws = check_case(SEG_GEOM, T, gpu, seed=9, logits=lg, bias=False, rsf=1.0)
+    assert ws["counts"].cpu().tolist() == counts
+
+
+SEG_WIDE = Geometry(256, 256, 256, 256, 8, 1, 1, ROUTING_SOFTMAX, "segments-wide")
+
+
+def test_segment_length_boundaries_streaming(gpu):
+    """The streaming kernels (T * top_k / E = 1) on expert segments of 0, 1, 2, 15, 16, 17, 31
+    and 32 pairs: the edges of their 16-row items, one and two items per segment."""
+    T = 32
+    counts = boundary_counts(T, E=SEG_WIDE.num_experts)
+    assert {15, 16, 17, 31, 32} <= set(counts)
+    lg = logits_for_counts(counts, T, SEG_WIDE.num_experts)
+    _, ws = check_case(SEG_WIDE, T, gpu, seed=10, logits=lg, bias=False, rsf=1.0)
     assert ws["counts"].cpu().tolist() == counts
 
 
@@ -507,9 +522,9 @@ def test_route_entry_matches_oracle(gpu, geom, T, off):
 
 # The operator captured in a HIP graph (serving loops replay one): the library records no memset
 # or allocation, so each replay over new inputs copied into the captured buffers must equal an
-# eager call on the same inputs bit for bit. T=64 selects the streaming kernels, T=2048 the large
-# tiles (T * top_k / E = 2 and 64).
-@pytest.mark.parametrize("T", [64, 2048])
+# eager call on the same inputs bit for bit. T=16 selects the streaming kernels, T=64 the
+# LDS-tiled GEMM1 and the streaming GEMM2, T=2048 the large tiles (T * top_k / E = 0, 2, 64).
+@pytest.mark.parametrize("T", [16, 64, 2048])
 def test_graph_replay_matches_eager(gpu, T):
     say(f"graph replay: mini-DS T={T}")
     w = weights_for(MINI_DS, gpu)[1]
