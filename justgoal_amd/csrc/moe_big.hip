@@ -200,12 +200,24 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm1_big_kernel(
              (uint32_t)kbi * T * 4);
       const __amdgpu_buffer_rsrc_t wres = make_rsrc(uniform(x.s.wbase), 2u * I * H);
       const uint32_t c0 = uniform(x.s.c0);
+      // An expert with a single M-tile reads each W13 byte once per call: its weight DMAs carry
+      // the non-temporal hint; experts with more M-tiles share their weight tiles in L2.
+      if (uniform(x.s.cnt) <= BM) {
 #pragma unroll
-      for (int j = 0; j < BI; ++j) {
-        const int grp = j >> 1;
-        const uint32_t row0 = grp < BN / 16 ? c0 + 16 * grp : I + c0 + 16 * (grp - BN / 16);
-        dma16(wres, &bring[slot][j * 1024], (j & 1) ? dma1 : dma0,
-              uniform(row0 * H + (uint32_t)kbi * kBlock));
+        for (int j = 0; j < BI; ++j) {
+          const int grp = j >> 1;
+          const uint32_t row0 = grp < BN / 16 ? c0 + 16 * grp : I + c0 + 16 * (grp - BN / 16);
+          dma16_stream(wres, &bring[slot][j * 1024], (j & 1) ? dma1 : dma0,
+                       uniform(row0 * H + (uint32_t)kbi * kBlock));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < BI; ++j) {
+          const int grp = j >> 1;
+          const uint32_t row0 = grp < BN / 16 ? c0 + 16 * grp : I + c0 + 16 * (grp - BN / 16);
+          dma16(wres, &bring[slot][j * 1024], (j & 1) ? dma1 : dma0,
+                uniform(row0 * H + (uint32_t)kbi * kBlock));
+        }
       }
     };
 #pragma unroll
@@ -517,10 +529,18 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
         dma16(cres, &aring[slot][j * 1024], aoff[j], (uint32_t)kbi * ARow);
       const __amdgpu_buffer_rsrc_t wres = make_rsrc(uniform(x.wbase), (uint32_t)H * I);
       const uint32_t h0 = uniform(x.h0);
+      // as in GEMM1: non-temporal weight DMAs for experts with a single M-tile
+      if (uniform(x.cnt) <= BM) {
 #pragma unroll
-      for (int j = 0; j < BI; ++j)
-        dma16(wres, &bring[slot][j * 1024], (j & 1) ? dma1 : dma0,
-              uniform((h0 + 16 * (j >> 1)) * (uint32_t)I + (uint32_t)kbi * kBlock));
+        for (int j = 0; j < BI; ++j)
+          dma16_stream(wres, &bring[slot][j * 1024], (j & 1) ? dma1 : dma0,
+                       uniform((h0 + 16 * (j >> 1)) * (uint32_t)I + (uint32_t)kbi * kBlock));
+      } else {
+#pragma unroll
+        for (int j = 0; j < BI; ++j)
+          dma16(wres, &bring[slot][j * 1024], (j & 1) ? dma1 : dma0,
+                uniform((h0 + 16 * (j >> 1)) * (uint32_t)I + (uint32_t)kbi * kBlock));
+      }
     };
 #pragma unroll
     for (int d = 0; d < D - 1; ++d) {

@@ -120,8 +120,9 @@ constexpr int kCachePolicyNT = 2;
 // ones (activation rows, C fragments). Measured on the weight-streaming and LDS-tiled kernels,
 // with three weight sets in rotation so no call finds its weights cached: DS-V3 T=64 call
 // 146.9 -> 134.5 us, T=256 203.9 -> 188.6 us, Qwen3-style T=128 499.6 -> 474.4 us. The large-tile
-// kernels, which reuse each weight tile across M-tiles through L2, got slower with it
-// (T=4096 GEMM1 217 -> 238 us) and keep the default policy.
+// kernels, which reuse each weight tile across M-tiles through L2, got slower with it on every
+// item (T=4096 GEMM1 217 -> 238 us); they use it only for experts with one M-tile (T=2048
+// 311 -> 303 us, T=4096 448 -> 441 us, Qwen3-style T=1024 574 -> 556 us).
 __device__ __forceinline__ void dma16_stream(__amdgpu_buffer_rsrc_t r, void* lds_base,
                                              uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds_base, 16, voff, soff, 0,
