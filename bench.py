@@ -42,10 +42,10 @@ PEAK_FP8_TFLOPS = 5000.0
 PEAK_BF16_TFLOPS = 2500.0
 STAGES = ("route", "permute", "gemm1_swiglu", "gemm2", "combine")
 # Kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (kStreamMaxRows, kBigRows,
-# kG2StreamMaxRows; tests/test_bench.py checks they match the source)
+# kG2TileMaxRows; tests/test_bench.py checks they match the source)
 GEMM1_STREAM_MAX_ROWS = 1
 GEMM1_BIG_ROWS = 64
-GEMM2_STREAM_MAX_ROWS = 4
+GEMM2_TILE_MAX_ROWS = 16
 
 
 def log(msg):
@@ -230,8 +230,9 @@ def gemm1_kernel_name(cfg):
 
 
 def gemm2_kernel_name(cfg):
-    """GEMM2: streaming up to GEMM2_STREAM_MAX_ROWS expected pairs per expert, large tiles above."""
-    return ("gemm2_stream_kernel" if _rows_hint(cfg) <= GEMM2_STREAM_MAX_ROWS
+    """GEMM2: LDS-tiled up to GEMM2_TILE_MAX_ROWS expected pairs per expert, large tiles above
+    (every bench geometry has I >= 384, which the LDS-tiled kernel needs)."""
+    return ("gemm2_tile_kernel" if _rows_hint(cfg) <= GEMM2_TILE_MAX_ROWS
             else "gemm2_big_kernel")
 
 

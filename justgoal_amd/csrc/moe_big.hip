@@ -71,10 +71,6 @@ __device__ __forceinline__ int map_item(const TileMapLds& tml, int item, int ite
 
 constexpr int vm_depth(int n) { return n > 63 ? 63 : n < 0 ? 0 : n; }
 
-// 16-byte chunk permutation of row n of the GEMM2 C tile in LDS (256-byte bf16 rows, one K
-// block; depends on n mod 16). The fragment read (lane = row n | group g, chunks 4g..4g+3) took
-// 21% less time with this permutation than with n & 15 in a ds_read_b128 probe.
-__device__ __forceinline__ int crow_swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
 
 // ---- GEMM1 ------------------------------------------------------------------------------------
 //

@@ -199,6 +199,11 @@ __device__ __forceinline__ uint32_t wblk_read_off(int lane, int half) {
   return n * 128 + 16 * ((2 * g + half) ^ wblk_swz(n));
 }
 
+// 16-byte chunk permutation of row n of a bf16 C tile in LDS (256-byte rows, one K block;
+// depends on n mod 16). The fragment read (lane = row n | group g, chunks 4g..4g+3) took 21%
+// less time with this permutation than with n & 15 in a ds_read_b128 probe.
+__device__ __forceinline__ int crow_swz(int row) { return ((row & 7) << 1) | ((row >> 3) & 1); }
+
 // Marks register values as used here, so the compiler completes their loads at this point (with
 // a counted wait) instead of at a later overwrite of the same registers.
 __device__ __forceinline__ void retire(float x) { asm volatile("" ::"v"(x)); }

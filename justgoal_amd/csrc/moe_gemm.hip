@@ -67,18 +67,19 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 }
 
 // Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from sweeps
-// over DS-V3 T = 16..16384 and Qwen3-style T = 128..1024: GEMM1 streams weights up to 1 expected
-// row, uses the LDS-tiled kernels up to 63 and the large tiles from 64; GEMM2 streams up to 4
-// and uses the large tiles above (their padding-row skip keeps part-filled 128-row tiles cheap;
-// the LDS-tiled GEMM2 lost to them everywhere). The streaming kernels' 16-row items re-stream an
-// expert's weights once per 16 rows, so they only win while segments are that short. With the
-// non-temporal weight stream of the streaming and LDS-tiled kernels, moving GEMM1's switch from
-// 4 to 1 and GEMM2's from 3 to 4 took DS-V3 T=64 from 133.5 to 132.1 us and T=128 from 185.6
-// to 171.3 us (two weight sets in rotation; T=16, 32, 192 and 256 unchanged).
+// over DS-V3 T = 16..16384 and Qwen3-style T = 128..1024. GEMM1 streams weights up to 1 expected
+// row, uses the LDS-tiled kernels up to 63 and the large tiles from 64. GEMM2 uses the LDS-tiled
+// kernel up to 16 expected rows (16-row tiles at <= 1, 32-row tiles above) and the large tiles
+// from 17; the streaming GEMM2 remains the fallback for shapes the tiled kernel does not take.
+// The streaming kernels' 16-row items re-stream an expert's weights once per 16 rows, so they
+// only win while segments are that short; the tiled GEMM2 shares one staged C tile among four
+// waves and streams each weight block once per 32 rows. Against streaming up to 4 rows and large
+// tiles above, it took DS-V3 T=16 from 64.6 to 61.7 us, T=64 from 131.8 to 126.1, T=128 from
+// 170.4 to 158.6, T=256 from 190.1 to 173.9 and Qwen3 T=128 from 467 to 434 (T=512, 16 rows:
+// level with the large tiles; 64-row tiled items from 17 rows lost to them, 299 vs 252 at 24).
 constexpr int kStreamMaxRows = 1;
 constexpr int kBigRows = 64;
-constexpr int kG2StreamMaxRows = 4;
-constexpr int kG2BigRows = 5;
+constexpr int kG2TileMaxRows = 16;
 
 constexpr int kTileMt8Rows = 256;
 
@@ -116,10 +117,12 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
                         Gemm2Out dst, int H, int I, int E_l, int max_pairs, int rows_hint,
                         hipStream_t stream) {
   if (max_pairs <= 0) return hipSuccess;
-  if (rows_hint <= kG2StreamMaxRows)
-    return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
-                               max_pairs, stream_mt(rows_hint), stream);
-  if (rows_hint >= kG2BigRows) {
+  if (rows_hint <= kG2TileMaxRows) {
+    const hipError_t t = launch_gemm2_tile(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
+                                           max_pairs, rows_hint <= 1 ? 1 : 2, stream);
+    if (t != hipErrorNotSupported) return t;
+  }
+  if (rows_hint > kG2TileMaxRows) {
     const hipError_t b = launch_gemm2_big(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
                                           max_pairs, stream);
     if (b != hipErrorNotSupported) return b;

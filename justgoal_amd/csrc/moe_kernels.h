@@ -73,6 +73,12 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
                              const float* s13, const int32_t* counts, const int32_t* offsets,
                              const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
                              int max_pairs, int mt, hipStream_t stream);
+// LDS-tiled GEMM2 (mt = 16-row sub-tiles per workgroup tile).
+hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* s2,
+                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
+                             Gemm2Out dst, int H, int I, int E_l, int max_pairs, int mt,
+                             hipStream_t stream);
+
 // Compute units of the current device, queried once per device (thread-safe); 256 when the
 // query fails. Sizes the persistent grids.
 int device_cu_count();

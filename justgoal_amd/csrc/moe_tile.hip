@@ -264,6 +264,223 @@ __global__ __launch_bounds__(256) void gemm1_tile_kernel(
   vm_wait<0>();  // no DMA may still target this workgroup's LDS when it retires
 }
 
+
+// ---- GEMM2 ------------------------------------------------------------------------------------
+//
+// A workgroup (4 waves) computes a BM x 64 tile of one expert's GEMM2 output (BM = 16*MT pairs):
+// the BM bf16 C rows of a K block are shared by the four waves through one LDS ring (each wave
+// DMAs a quarter of them; the tile's buffer resource ends at the segment, so padding rows are
+// never fetched), each wave streams the W2 rows of its own 16 output columns into a private ring
+// (non-temporal: read once per call). Same per-step barrier protocol as GEMM1 above; MFMA form,
+// scales and epilogue as in the streaming GEMM2.
+
+template <int MT>
+struct T2Item {
+  const uint8_t* wbase;   // the expert's W2
+  uint32_t wsoff;         // h0 * I (this wave's first W2 row)
+  LaneScales sc;          // weight scales of this wave's 128-row W2 block
+  float wgt[MT];          // routing weight of the lane's row in each sub-tile
+  int dst[MT];            // destination row code (pair_dst) of that row
+  const uint16_t* cbase;  // C row of the tile's first pair
+  uint32_t crec;          // bytes of C from cbase to the segment's end
+  int m0, cnt, seg, h0;
+};
+
+template <int MT, int D>
+__global__ __launch_bounds__(256) void gemm2_tile_kernel(
+    const uint16_t* __restrict__ C, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    const float* __restrict__ sorted_w, Gemm2Out dst, int H, int I, int E_l, int max_pairs) {
+  static_assert(D >= 3, "the prefetch lead is D-1 blocks");
+  constexpr int BM = 16 * MT;
+  constexpr int ARow = 2 * kBlock;  // bf16 C bytes per row per K block
+  constexpr int AI = MT;            // C DMA instructions per wave per step (4 rows x 256 B each)
+  constexpr int OPS = AI + 2;       // vector-memory operations per wave per step
+  constexpr int MW = 2 * MT + 2;    // metadata dwords per lane
+  __shared__ __attribute__((aligned(16))) uint32_t mring[kWaves][MW][kWave];
+  __shared__ __attribute__((aligned(16))) uint8_t bring[kWaves][D][kWBlk];
+  __shared__ __attribute__((aligned(16))) uint8_t aring[D][BM * ARow];
+
+  const int lane = threadIdx.x & (kWave - 1), w = wave_id();
+  const int r16 = lane & 15, g = lane >> 4;
+  const int NNT = H / 64, NKB = I / kBlock;
+  TileMap tm;
+  tm.init(counts, offsets, E_l, BM);
+  const int items = tm.total * NNT;
+  int it = uniform((int)blockIdx.x);
+  if (it >= items) return;  // whole workgroup
+  const int stride = gridDim.x;
+
+  const uint32_t dma0 = wblk_dma_off(lane, 0, I), dma1 = wblk_dma_off(lane, 1, I);
+  const uint32_t rd0 = wblk_read_off(lane, 0), rd1 = wblk_read_off(lane, 1);
+  uint8_t* my_bring = &bring[w][0][0];
+  // C DMA instruction i of wave w covers tile rows 4*(w*AI + i) + lane/16, chunk position
+  // lane & 15 holding chunk (lane & 15) ^ crow_swz(row); offsets relative to the tile's first row.
+  uint32_t aoff[AI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int row = 4 * (w * AI + i) + (lane >> 4);
+    aoff[i] = (uint32_t)row * I * 2 + 16 * ((lane & 15) ^ crow_swz(row));
+  }
+
+  const __amdgpu_buffer_rsrc_t wgtres = make_rsrc(sorted_w, (uint32_t)max_pairs * 4);
+  const __amdgpu_buffer_rsrc_t dstres = make_rsrc(dst.pair_dst, (uint32_t)max_pairs * 4);
+  const __amdgpu_buffer_rsrc_t s2res = make_rsrc(s2, (uint32_t)E_l * (H / kBlock) * NKB * 4);
+  uint32_t* my_meta = &mring[w][0][0];
+  auto meta = [&](int item, T2Item<MT>& x) {
+    item = uniform(item);
+    const int tile = item / NNT, nt = item % NNT;
+    const int e = tm.find(tile, BM, x.m0, x.cnt, x.seg);
+    x.m0 = uniform(x.m0);
+    x.cnt = uniform(x.cnt);
+    x.seg = uniform(x.seg);
+    x.h0 = uniform(nt * 64 + w * 16);
+    x.wbase = uniform(w2 + (size_t)e * H * I);
+    x.wsoff = uniform((uint32_t)x.h0 * I);
+    x.cbase = uniform(C + (size_t)(x.seg + x.m0) * I);
+    x.crec = uniform((uint32_t)(x.cnt - x.m0) * I * 2);
+    const int last = x.cnt - 1;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = x.m0 + mt * 16 + r16;
+      const uint32_t p = 4u * (x.seg + (r < last ? r : last));
+      dma4(wgtres, my_meta + mt * kWave, p, 0);
+      dma4(dstres, my_meta + (MT + mt) * kWave, p, 0);
+    }
+    const uint32_t so = uniform((uint32_t)((e * (H / kBlock) + x.h0 / kBlock) * NKB) * 4);
+    dma4(s2res, my_meta + 2 * MT * kWave, 4u * lane, so);
+    dma4(s2res, my_meta + (2 * MT + 1) * kWave, 4u * (lane + kWave), so);
+  };
+  auto finish = [&](T2Item<MT>& x) {
+    const uint32_t mb = lds_addr(my_meta) + 4 * lane;
+    float v[MW];
+#pragma unroll
+    for (int j = 0; j < MW; ++j) v[j] = ds_read4f(mb + j * 4 * kWave);
+    lds_wait_all();
+#pragma unroll
+    for (int j = 0; j < MW; ++j) lds_fence(v[j]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      x.wgt[mt] = v[mt];
+      x.dst[mt] = __float_as_int(v[MT + mt]);
+    }
+    x.sc.v0 = v[2 * MT];
+    x.sc.v1 = v[2 * MT + 1];
+  };
+
+  T2Item<MT> cur, nxt, nn;
+  meta(it, cur);
+  vm_wait<0>();
+  finish(cur);
+  int it_n = it + stride;
+  meta(it_n < items ? it_n : it, nxt);
+  vm_wait<0>();
+  finish(nxt);
+
+  auto issue = [&](bool second, int kbi, int slot) {
+    const __amdgpu_buffer_rsrc_t cres = make_rsrc(uniform(second ? nxt.cbase : cur.cbase),
+                                                  uniform(second ? nxt.crec : cur.crec));
+#pragma unroll
+    for (int i = 0; i < AI; ++i)
+      dma16(cres, &aring[slot][(w * AI + i) * 1024], aoff[i], (uint32_t)kbi * ARow);
+    const __amdgpu_buffer_rsrc_t wres =
+        make_rsrc(uniform(second ? nxt.wbase : cur.wbase), (uint32_t)H * I);
+    const uint32_t ws = uniform((second ? nxt.wsoff : cur.wsoff) + (uint32_t)kbi * kBlock);
+    uint8_t* b = my_bring + slot * kWBlk;
+    dma16_stream(wres, b, dma0, ws);
+    dma16_stream(wres, b + 1024, dma1, ws);
+  };
+
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    issue(false, d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  int slot = 0;
+  for (;;) {
+    const int it_nn = it_n + stride;
+    meta(it_nn < items ? it_nn : (it_n < items ? it_n : it), nn);
+
+    v4f acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    int kb = 0;
+    do {
+      {
+        const int d = slot;
+        vm_wait<vm_depth((D - 2) * OPS)>();  // this wave's DMAs of block kb are done
+        __builtin_amdgcn_s_barrier();        // everyone's are; slot d-1 is no longer read
+        const int kn = kb + D - 1;
+        const bool second = kn >= NKB;
+        issue(second, second ? kn - NKB : kn, d == 0 ? D - 1 : d - 1);
+        __builtin_amdgcn_sched_barrier(0);
+
+        const uint32_t bb = lds_addr(my_bring + d * kWBlk);
+        const uint32_t ab = lds_addr(&aring[d][0]);
+        v4u wl = ds_read16(bb + rd0), wh = ds_read16(bb + rd1);
+        v4u a[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int row = mt * 16 + r16;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            a[mt][c] = ds_read16(ab + row * ARow + 16 * ((4 * g + c) ^ crow_swz(row)));
+        }
+        lds_wait_all();
+        lds_fence(wl);
+        lds_fence(wh);
+        const uint32_t wv[8] = {wl[0], wl[1], wl[2], wl[3], wh[0], wh[1], wh[2], wh[3]};
+        v8bf bw[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v2bf p0, p1, p2, p3;
+          fp8x4_to_bf16x4((int)wv[2 * c], p0, p1);
+          fp8x4_to_bf16x4((int)wv[2 * c + 1], p2, p3);
+          bw[c] = v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        }
+        const float sw = cur.sc.get(kb);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          v4f t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            lds_fence(a[mt][c]);
+            t = mfma_bf16_16x16x32(bw[c], __builtin_bit_cast(v8bf, a[mt][c]), t);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mt][i] = fmaf(t[i], sw, acc[mt][i]);
+        }
+      }
+      slot = slot + 1 == D ? 0 : slot + 1;
+      ++kb;
+    } while (kb < NKB);
+    vm_wait<vm_depth((D - 1) * OPS)>();  // the next item's metadata DMAs have landed
+    finish(nn);
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = cur.m0 + mt * 16 + r16;
+      if (r < cur.cnt) {
+        const float wp = cur.wgt[mt];
+        const int dd = cur.dst[mt];
+        uint16_t* row = dd >= 0 ? dst.out + (size_t)dd * H : dst.partial + (size_t)(-1 - dd) * H;
+        const uint32_t h01 = (uint32_t)float_to_bf16_bits(acc[mt][0] * wp) |
+                             ((uint32_t)float_to_bf16_bits(acc[mt][1] * wp) << 16);
+        const uint32_t h23 = (uint32_t)float_to_bf16_bits(acc[mt][2] * wp) |
+                             ((uint32_t)float_to_bf16_bits(acc[mt][3] * wp) << 16);
+        *(uint2*)(row + cur.h0 + 4 * g) = uint2{h01, h23};
+      }
+    }
+    if (it_n >= items) break;
+    it = it_n;
+    it_n = it_nn;
+    cur = nxt;
+    nxt = nn;
+  }
+  vm_wait<0>();  // no DMA may still target this workgroup's LDS when it retires
+}
+
 }  // namespace
 
 static int tile_grid(int per_cu, long long max_items) {
@@ -286,6 +503,9 @@ static inline long long tile_count(int max_pairs, int bm, int E_l) {
 // Ring depths (lead D-1 blocks). D = 3 keeps two workgroups per CU within the 160 KiB of LDS,
 // which measured faster than deeper rings at one workgroup per CU.
 constexpr int kG1tD = 3;
+// GEMM2's K blocks are half as many bytes of weight per step (bf16 C is the larger operand), so
+// four slots still fit two workgroups per CU; D = 4 measured ahead of D = 3 at 2..8 rows/expert.
+constexpr int kG2tD = 4;
 
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                              const float* s13, const int32_t* counts, const int32_t* offsets,
@@ -306,6 +526,26 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
   if (mt <= 4) JG_G1T(4, kG1tD)
   JG_G1T(8, (kG1tD > 4 ? 4 : kG1tD))  // a 128-row tile leaves room for 4 slots
 #undef JG_G1T
+}
+
+hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* s2,
+                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
+                             Gemm2Out dst, int H, int I, int E_l, int max_pairs, int mt,
+                             hipStream_t stream) {
+#define JG_G2T(MT, D)                                                                           \
+  {                                                                                             \
+    if (I / kBlock < (D) - 1 || H % 64 != 0) return hipErrorNotSupported;                      \
+    constexpr int lds = kWaves * D * kWBlk + D * 16 * MT * 2 * kBlock +                         \
+                        kWaves * (2 * MT + 2) * kWave * 4;                                      \
+    const int grid =                                                                            \
+        tile_grid(tile_groups_per_cu(lds), tile_count(max_pairs, 16 * MT, E_l) * (H / 64));     \
+    gemm2_tile_kernel<MT, D><<<grid, kWaves * kWave, 0, stream>>>(                              \
+        C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs);                       \
+    return hipGetLastError();                                                                   \
+  }
+  if (mt <= 1) JG_G2T(1, kG2tD)
+  JG_G2T(2, kG2tD)
+#undef JG_G2T
 }
 
 }  // namespace jgmoe

@@ -56,15 +56,18 @@ def test_kernel_family_thresholds_match_the_library_source():
     src = open(os.path.join(ROOT, "justgoal_amd", "csrc", "moe_gemm.hip")).read()
     stream = int(re.search(r"constexpr int kStreamMaxRows = (\d+);", src).group(1))
     big = int(re.search(r"constexpr int kBigRows = (\d+);", src).group(1))
-    g2 = int(re.search(r"constexpr int kG2StreamMaxRows = (\d+);", src).group(1))
+    g2 = int(re.search(r"constexpr int kG2TileMaxRows = (\d+);", src).group(1))
     assert (bench.GEMM1_STREAM_MAX_ROWS, bench.GEMM1_BIG_ROWS) == (stream, big)
-    assert bench.GEMM2_STREAM_MAX_ROWS == g2
+    assert bench.GEMM2_TILE_MAX_ROWS == g2
     from justgoal_amd import inputs as jin
     names = {n: bench.gemm1_kernel_name(c) for n, c in jin.CONFIGS.items()}
     assert names["ds_t16"] == "gemm1_stream_kernel"
     assert names["ds_t64"] == "gemm1_tile_kernel"
     assert names["ds_t512"] == "gemm1_tile_kernel"
     assert names["ds_t4096"] == "gemm1_big_kernel"
+    g2names = {n: bench.gemm2_kernel_name(c) for n, c in jin.CONFIGS.items()}
+    assert g2names["ds_t16"] == g2names["ds_t512"] == "gemm2_tile_kernel"
+    assert g2names["ds_t1024"] == "gemm2_big_kernel"
 
 
 def test_gemm2_unit_figures_and_roofline_bound():

@@ -259,8 +259,9 @@ def test_definition_token_counts_via_reference_binding(gpu, T):
 
 
 # Qwen3 geometry (H=4096, I=1536: 12 K blocks in GEMM2) across the kernel families:
-# T * top_k / E = 0.06 and 0.5 stream weights in both GEMMs, 4 uses the LDS-tiled GEMM1 and the
-# streaming GEMM2, ~19 the LDS-tiled GEMM1 and the large-tile GEMM2.
+# T * top_k / E = 0.06 and 0.5 stream weights in GEMM1 and use the LDS-tiled GEMM2 with 16-row
+# tiles, 4 uses the LDS-tiled GEMM1 and the LDS-tiled GEMM2 with 32-row tiles, ~19 the LDS-tiled
+# GEMM1 and the large-tile GEMM2.
 @pytest.mark.parametrize("T", [1, 8, 64, 300])
 def test_qwen3_small_and_mid_batches(gpu, T):
     say(f"qwen3 T={T}")
@@ -327,6 +328,9 @@ def test_bound_call_matches_run(gpu):
 
 
 SEG_GEOM = Geometry(256, 256, 64, 64, 8, 1, 1, ROUTING_SOFTMAX, "segments")
+# I = 384 (3 K blocks) is the smallest intermediate size the LDS-tiled GEMM2 takes (its 4-slot
+# ring leads by 3 blocks); at I = 256 GEMM2 falls back to the streaming kernel.
+SEG_GEOM_G2T = Geometry(256, 384, 64, 64, 8, 1, 1, ROUTING_SOFTMAX, "segments-i384")
 
 
 def logits_for_counts(counts, T, E, top_k=8):
@@ -359,28 +363,36 @@ def boundary_counts(T, E=64, top_k=8):
     return counts
 
 
-@pytest.mark.parametrize("T", [128, 256, 512, 1024])
-def test_segment_length_boundaries(gpu, T):
+@pytest.mark.parametrize("geom,T", [(SEG_GEOM, 128), (SEG_GEOM, 256), (SEG_GEOM, 512),
+                                    (SEG_GEOM, 1024), (SEG_GEOM_G2T, 64), (SEG_GEOM_G2T, 128)],
+                         ids=lambda v: getattr(v, "name", v))
+def test_segment_length_boundaries(gpu, geom, T):
     """Expert segments of exactly 1, 15, 16, 17, 31, 32, 33, ... pairs (and empty experts): the
-    tile edges of the LDS-tile (T=128, 256) and large-tile (T=512, 1024) kernels,
-    including large-tile waves whose rows of a tile are all padding."""
+    tile edges of the LDS-tiled GEMM1 (T=128, 256), the large-tile kernels (T=512, 1024, and
+    GEMM2 from T=256), including large-tile waves whose rows of a tile are all padding, and of
+    the LDS-tiled GEMM2's 32-row tiles (I=384, T=64 and 128: 8 and 16 expected rows)."""
     counts = boundary_counts(T)
-    lg = logits_for_counts(counts, T, SEG_GEOM.num_experts)
-    _, ws = check_case(SEG_GEOM, T, gpu, seed=9, logits=lg, bias=False, rsf=1.0)
+    lg = logits_for_counts(counts, T, geom.num_experts)
+    _, ws = check_case(geom, T, gpu, seed=9, logits=lg, bias=False, rsf=1.0)
     assert ws["counts"].cpu().tolist() == counts
 
 
 SEG_WIDE = Geometry(256, 256, 256, 256, 8, 1, 1, ROUTING_SOFTMAX, "segments-wide")
 
 
-def test_segment_length_boundaries_streaming(gpu):
-    """The streaming kernels (T * top_k / E = 1) on expert segments of 0, 1, 2, 15, 16, 17, 31
-    and 32 pairs: the edges of their 16-row items, one and two items per segment."""
+SEG_WIDE_G2T = Geometry(256, 384, 256, 256, 8, 1, 1, ROUTING_SOFTMAX, "segments-wide-i384")
+
+
+@pytest.mark.parametrize("geom", [SEG_WIDE, SEG_WIDE_G2T], ids=lambda g: g.name)
+def test_segment_length_boundaries_streaming(gpu, geom):
+    """T * top_k / E = 1 on expert segments of 0, 1, 2, 15, 16, 17, 31 and 32 pairs: the edges
+    of the 16-row items of the streaming kernels (both GEMMs at I=256) and of the LDS-tiled
+    GEMM2's 16-row tiles (I=384), one and two items per segment."""
     T = 32
-    counts = boundary_counts(T, E=SEG_WIDE.num_experts)
+    counts = boundary_counts(T, E=geom.num_experts)
     assert {15, 16, 17, 31, 32} <= set(counts)
-    lg = logits_for_counts(counts, T, SEG_WIDE.num_experts)
-    _, ws = check_case(SEG_WIDE, T, gpu, seed=10, logits=lg, bias=False, rsf=1.0)
+    lg = logits_for_counts(counts, T, geom.num_experts)
+    _, ws = check_case(geom, T, gpu, seed=10, logits=lg, bias=False, rsf=1.0)
     assert ws["counts"].cpu().tolist() == counts
 
 
@@ -523,16 +535,18 @@ def test_route_entry_matches_oracle(gpu, geom, T, off):
 # The operator captured in a HIP graph (serving loops replay one): the library records no memset
 # or allocation, so each replay over new inputs copied into the captured buffers must equal an
 # eager call on the same inputs bit for bit. T=16 selects the streaming kernels, T=64 the
-# LDS-tiled GEMM1 and the streaming GEMM2, T=2048 the large tiles (T * top_k / E = 0, 2, 64).
-@pytest.mark.parametrize("T", [16, 64, 2048])
-def test_graph_replay_matches_eager(gpu, T):
-    say(f"graph replay: mini-DS T={T}")
-    w = weights_for(MINI_DS, gpu)[1]
-    static = to_dev(jin.make_activations(MINI_DS, T, seed=20), gpu)
+# LDS-tiled GEMM1 and the streaming GEMM2 (I = 256 is below the LDS-tiled GEMM2's minimum), T=2048
+# the large tiles (T * top_k / E = 0, 2, 64); mini-softmax (I = 384) T=64 the LDS-tiled GEMM2.
+@pytest.mark.parametrize("geom,T", [(MINI_DS, 16), (MINI_DS, 64), (MINI_DS, 2048),
+                                    (MINI_SOFTMAX, 64)], ids=lambda v: getattr(v, "name", v))
+def test_graph_replay_matches_eager(gpu, geom, T):
+    say(f"graph replay: {geom.name} T={T}")
+    w = weights_for(geom, gpu)[1]
+    static = to_dev(jin.make_activations(geom, T, seed=20), gpu)
     kw = dict(gemm1_weights=w[0], gemm1_weights_scale=w[1], gemm2_weights=w[2],
               gemm2_weights_scale=w[3], local_expert_offset=0, routed_scaling_factor=2.5,
-              geometry=MINI_DS)
-    out = torch.empty(T, MINI_DS.hidden, dtype=torch.bfloat16, device=gpu)
+              geometry=geom)
+    out = torch.empty(T, geom.hidden, dtype=torch.bfloat16, device=gpu)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -543,7 +557,7 @@ def test_graph_replay_matches_eager(gpu, T):
     with torch.cuda.graph(g, stream=s):
         run(**static, **kw, output=out)
     for seed in (21, 22, 23):
-        fresh = to_dev(jin.make_activations(MINI_DS, T, seed=seed), gpu)
+        fresh = to_dev(jin.make_activations(geom, T, seed=seed), gpu)
         for k, v in fresh.items():
             static[k].copy_(v)
         torch.cuda.synchronize()
