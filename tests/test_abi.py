@@ -53,15 +53,27 @@ def test_workspace_bytes_as_the_reference_binds_it():
         assert L.moe_workspace_bytes(T) == _lib.workspace_layout(DS_V3, T)["total"]
 
 
+def test_region_names_match_the_header_enum():
+    """_lib.WS_REGIONS / MOE_WS_NUM_REGIONS mirror the MOE_WS_* enum of include/justgoal_moe.h
+    in order: moe_workspace_layout writes MOE_WS_NUM_REGIONS + 1 offsets into the caller's
+    array, so a shorter Python array would be overrun."""
+    import re
+    hdr = open(os.path.join(ROOT, "include", "justgoal_moe.h")).read()
+    body = hdr[hdr.index("MOE_WS_TOPK_IDX = 0"):hdr.index("MOE_WS_NUM_REGIONS")]
+    names = re.findall(r"MOE_WS_([A-Z_]+)", body)
+    assert len(names) == _lib.MOE_WS_NUM_REGIONS == len(_lib.WS_REGIONS)
+    assert [n.lower() for n in names] == [r.lower() for r in _lib.WS_REGIONS]
+
+
 def test_layout_regions_ordered_and_aligned():
-    lay = _lib.workspace_layout(QWEN3, 1000)
+    lay = _lib.workspace_layout(QWEN3, 1024)
     offs = [lay[n] for n in _lib.WS_REGIONS] + [lay["total"]]
     assert offs == sorted(offs)
     assert all(o % 256 == 0 for o in offs)
     # C region holds Np x I bf16, partial T x (k - 1) x H bf16, pair_dst Np int32
-    Np = 1000 * 8
+    Np = 1024 * 8
     assert lay["partial"] - lay["C"] >= Np * QWEN3.intermediate * 2
-    assert lay["chunk_counts"] - lay["partial"] >= 1000 * 7 * QWEN3.hidden * 2
+    assert lay["chunk_counts"] - lay["partial"] >= 1024 * 7 * QWEN3.hidden * 2
     assert lay["total"] - lay["pair_dst"] >= Np * 4
 
 
