@@ -390,16 +390,50 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __shared__ int off[kMaxLocal + 1];
   const int t0 = blockIdx.x * kPlaceTokens;
   const int row0 = t0 / route_tokens_per_group(T);  // first count row of this chunk
-  // Column sums of the count table: thread (e, slice) adds every n_slices-th row of column e;
-  // loads are issued eight at a time so they overlap.
-  const int n_slices = max(1, (int)blockDim.x / E_l);
-  const int e = threadIdx.x % E_l, slice = threadIdx.x / E_l;
+  // Column sums of the count table. For tables of 64 rows or more (T > 256) and E_l a multiple
+  // of 4, thread (q, slice) adds columns 4q..4q+3 of every n_slices-th row with 16-byte loads,
+  // sixteen rows in flight (T = 16384: 32 rows per thread instead of 128; permute 27.8 -> 12.8 us,
+  // T = 4096 13.9 -> 11.2 us); otherwise thread (e, slice) adds column e, eight rows in flight.
+  const bool quads = (E_l & 3) == 0 && n_rows >= 64;
+  const int cols = quads ? E_l / 4 : E_l;
+  const int n_slices = max(1, (int)blockDim.x / cols);
+  const int e = threadIdx.x % cols, slice = threadIdx.x / cols;
   if (threadIdx.x < E_l) {
     total[threadIdx.x] = 0;
     before[threadIdx.x] = 0;
   }
   __syncthreads();
-  if (slice < n_slices) {
+  if (quads && slice < n_slices) {
+    int4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+    for (int r0 = slice; r0 < n_rows; r0 += 16 * n_slices) {
+      int4 h[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int r = r0 + u * n_slices;
+        h[u] = r < n_rows ? *(const int4*)(hist + (size_t)r * E_l + 4 * e) : int4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const bool bf = (r0 + u * n_slices) < row0;
+        a.x += h[u].x;
+        a.y += h[u].y;
+        a.z += h[u].z;
+        a.w += h[u].w;
+        b.x += bf ? h[u].x : 0;
+        b.y += bf ? h[u].y : 0;
+        b.z += bf ? h[u].z : 0;
+        b.w += bf ? h[u].w : 0;
+      }
+    }
+    atomicAdd(&total[4 * e], a.x);
+    atomicAdd(&total[4 * e + 1], a.y);
+    atomicAdd(&total[4 * e + 2], a.z);
+    atomicAdd(&total[4 * e + 3], a.w);
+    atomicAdd(&before[4 * e], b.x);
+    atomicAdd(&before[4 * e + 1], b.y);
+    atomicAdd(&before[4 * e + 2], b.z);
+    atomicAdd(&before[4 * e + 3], b.w);
+  } else if (!quads && slice < n_slices) {
     int a = 0, b = 0;
     for (int r0 = slice; r0 < n_rows; r0 += 8 * n_slices) {
       int h[8];
