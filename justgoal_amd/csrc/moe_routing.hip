@@ -206,34 +206,32 @@ __device__ __forceinline__ void route_token(const float (&x)[VPL], const float (
     }
   }
 
-  float w[kMaxTopK];
+  // Lane k < top_k keeps selection k; the weights take the same operations per selection as the
+  // definition, each lane evaluating only its own division (and, for softmax, its own exp).
+  float mine = sel_val[0];
+  int idx = sel_idx[0];
+#pragma unroll
+  for (int k = 1; k < kMaxTopK; ++k)
+    if (lane == k) {
+      mine = sel_val[k];
+      idx = sel_idx[k];
+    }
+  out_idx = idx;
   if (METHOD == ROUTING_DS) {
     float sum = 0.0f;
 #pragma unroll
     for (int k = 0; k < kMaxTopK; ++k)
       if (k < top_k) sum += sel_val[k];
     sum += 1e-20f;
-#pragma unroll
-    for (int k = 0; k < kMaxTopK; ++k) w[k] = sel_val[k] / sum * rsf;
+    out_w = mine / sum * rsf;
   } else {
-    float ex[kMaxTopK];
+    const float ex = exp_f32(mine - sel_val[0]);
     float sum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMaxTopK; ++k) {
-      ex[k] = exp_f32(sel_val[k] - sel_val[0]);
-      if (k < top_k) sum += ex[k];
-    }
-#pragma unroll
-    for (int k = 0; k < kMaxTopK; ++k) w[k] = ex[k] / sum;
+    for (int k = 0; k < kMaxTopK; ++k)
+      if (k < top_k) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), k));
+    out_w = ex / sum;
   }
-  out_idx = sel_idx[0];
-  out_w = w[0];
-#pragma unroll
-  for (int k = 1; k < kMaxTopK; ++k)
-    if (lane == k) {
-      out_idx = sel_idx[k];
-      out_w = w[k];
-    }
 }
 
 
