@@ -809,6 +809,18 @@ constexpr int kB2Ns = 4;
 constexpr int kB2Wm = 4;
 constexpr int kB2Wn = 2;
 constexpr int kB2D = 3;
+// GEMM2 for 17..63 expected rows per expert: 64-row tiles (2 x 4 waves of 32 x 32, NS = 2) in a
+// 4-slot ring (146 KB of LDS). Against the 128-row tiles, whole call, two weight sets in
+// rotation, results bit-identical: DS-V3 T=768 252.1 -> 236.6 us, T=1024 260.6 -> 249.8,
+// T=1280 283.0 -> 275.4, T=1536 310.0 -> 306.9, T=1792 344.1 -> 339.9; Qwen3-style T=512 503.3 ->
+// 486.0, T=640 515.0 -> 504.0, T=768 541.2 -> 534.4. From 64 rows the 128-row tiles stay ahead
+// (DS-V3 T=2048 299.8 against 304.6, Qwen3-style T=1024 554.0 against 568.4). A 3-slot ring
+// was 0.4-1.5% behind the 4-slot one everywhere.
+constexpr int kB2TallRows = 64;
+constexpr int kB2ShortWm = 2;
+constexpr int kB2ShortWn = 4;
+constexpr int kB2ShortNs = 2;
+constexpr int kB2ShortD = 4;
 
 hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                             const float* s13, const int32_t* counts, const int32_t* offsets,
@@ -824,16 +836,31 @@ hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s2,
-                            const int32_t* counts, const int32_t* offsets, const float* sorted_w,
-                            Gemm2Out dst, int H, int I, int E_l, int max_pairs,
-                            hipStream_t stream) {
-  constexpr int BN = 16 * kB2Ns * kB2Wn;
-  if (H % BN != 0 || I / kBlock < kB2D - 1) return hipErrorNotSupported;
-  const int grid = big_grid(big_tiles(max_pairs, 16 * kB2Ms * kB2Wm, E_l) * (H / BN));
-  gemm2_big_kernel<kB2Ms, kB2Ns, kB2D, kB2Wm, kB2Wn><<<grid, (kB2Wm * kB2Wn + 1) * kWave, 0, stream>>>(
+template <int MS, int NS, int D, int WM, int WN>
+static hipError_t launch_gemm2_big_t(const uint16_t* C, const uint8_t* w2, const float* s2,
+                                     const int32_t* counts, const int32_t* offsets,
+                                     const float* sorted_w, Gemm2Out dst, int H, int I, int E_l,
+                                     int max_pairs, hipStream_t stream) {
+  constexpr int BN = 16 * NS * WN;
+  if (H % BN != 0 || I / kBlock < D - 1) return hipErrorNotSupported;
+  const int grid = big_grid(big_tiles(max_pairs, 16 * MS * WM, E_l) * (H / BN));
+  gemm2_big_kernel<MS, NS, D, WM, WN><<<grid, (WM * WN + 1) * kWave, 0, stream>>>(
       C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs, kSchedGemm2);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s2,
+                            const int32_t* counts, const int32_t* offsets, const float* sorted_w,
+                            Gemm2Out dst, int H, int I, int E_l, int max_pairs, int rows_hint,
+                            hipStream_t stream) {
+  if (rows_hint < kB2TallRows) {
+    const hipError_t e = launch_gemm2_big_t<kB2Ms, kB2ShortNs, kB2ShortD, kB2ShortWm, kB2ShortWn>(
+        C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs, stream);
+    if (e != hipErrorNotSupported) return e;  // I = 256: the 4-slot ring needs 3 K blocks
+  }
+  return launch_gemm2_big_t<kB2Ms, kB2Ns, kB2D, kB2Wm, kB2Wn>(C, w2, s2, counts, offsets,
+                                                              sorted_w, dst, H, I, E_l,
+                                                              max_pairs, stream);
 }
 
 }  // namespace jgmoe

@@ -69,17 +69,22 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 // Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from sweeps
 // over DS-V3 T = 16..16384 and Qwen3-style T = 128..1024. GEMM1 streams weights up to 1 expected
 // row, uses the LDS-tiled kernels up to 63 and the large tiles from 64. GEMM2 uses the LDS-tiled
-// kernel up to 16 expected rows (16-row tiles at <= 1, 32-row tiles above) and the large tiles
-// from 17; the streaming GEMM2 remains the fallback for shapes the tiled kernel does not take.
+// kernel up to 7 expected rows (16-row tiles at <= 1, 32-row tiles above) and the large-tile
+// kernel from 8 (64-row tiles up to 63, 128-row tiles from 64); the streaming GEMM2 remains the
+// fallback for shapes the tiled kernel does not take.
 // The streaming kernels' 16-row items re-stream an expert's weights once per 16 rows, so they
 // only win while segments are that short; the tiled GEMM2 shares one staged C tile among four
 // waves and streams each weight block once per 32 rows. Against streaming up to 4 rows and large
 // tiles above, it took DS-V3 T=16 from 64.6 to 61.7 us, T=64 from 131.8 to 126.1, T=128 from
 // 170.4 to 158.6, T=256 from 190.1 to 173.9 and Qwen3 T=128 from 467 to 434 (T=512, 16 rows:
 // level with the large tiles; 64-row tiled items from 17 rows lost to them, 299 vs 252 at 24).
+// The 64-row large tiles (moe_big.hip) then moved the switch from 16 to 7 expected rows: DS-V3
+// T=256 (8 rows) 172.2 -> 170.4 us, T=384 186.1 -> 178.9, T=512 226.4 -> 210.0; Qwen3-style
+// T=128 432.3 -> 428.6, T=256 461.7 -> 452.2; at 6 rows the tiled kernel stays ahead (DS-V3 T=192
+// 163.5 against 168.3).
 constexpr int kStreamMaxRows = 1;
 constexpr int kBigRows = 64;
-constexpr int kG2TileMaxRows = 16;
+constexpr int kG2TileMaxRows = 7;
 
 constexpr int kTileMt8Rows = 256;
 
@@ -124,7 +129,7 @@ hipError_t launch_gemm2(const uint16_t* C, const uint8_t* w2, const float* s2,
   }
   if (rows_hint > kG2TileMaxRows) {
     const hipError_t b = launch_gemm2_big(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l,
-                                          max_pairs, stream);
+                                          max_pairs, rows_hint, stream);
     if (b != hipErrorNotSupported) return b;
   }
   return launch_gemm2_stream(C, w2, s2, counts, offsets, sorted_w, dst, H, I, E_l, max_pairs,

@@ -65,7 +65,7 @@ hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint
                             int max_pairs, hipStream_t stream);
 hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s2,
                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
-                            Gemm2Out dst, int H, int I, int E_l, int max_pairs,
+                            Gemm2Out dst, int H, int I, int E_l, int max_pairs, int rows_hint,
                             hipStream_t stream);
 
 // LDS-tiled variants for longer segments (mt = 16-row sub-tiles per workgroup tile).

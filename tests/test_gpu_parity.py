@@ -364,13 +364,16 @@ def boundary_counts(T, E=64, top_k=8):
 
 
 @pytest.mark.parametrize("geom,T", [(SEG_GEOM, 128), (SEG_GEOM, 256), (SEG_GEOM, 512),
-                                    (SEG_GEOM, 1024), (SEG_GEOM_G2T, 64), (SEG_GEOM_G2T, 128)],
+                                    (SEG_GEOM, 1024), (SEG_GEOM_G2T, 48), (SEG_GEOM_G2T, 64),
+                                    (SEG_GEOM_G2T, 128), (SEG_GEOM_G2T, 256)],
                          ids=lambda v: getattr(v, "name", v))
 def test_segment_length_boundaries(gpu, geom, T):
     """Expert segments of exactly 1, 15, 16, 17, 31, 32, 33, ... pairs (and empty experts): the
     tile edges of the LDS-tiled GEMM1 (T=128, 256), the large-tile kernels (T=512, 1024, and
-    GEMM2 from T=256), including large-tile waves whose rows of a tile are all padding, and of
-    the LDS-tiled GEMM2's 32-row tiles (I=384, T=64 and 128: 8 and 16 expected rows)."""
+    GEMM2 from T=256), including large-tile waves whose rows of a tile are all padding; at
+    I=384 the LDS-tiled GEMM2's 32-row tiles (T=48: 6 expected rows) and the large-tile GEMM2's
+    64-row tiles in their 4-slot ring (T=64, 128, 256: 8, 16 and 32 expected rows; at I=256 that
+    shape falls back to the 128-row tiles)."""
     counts = boundary_counts(T)
     lg = logits_for_counts(counts, T, geom.num_experts)
     _, ws = check_case(geom, T, gpu, seed=9, logits=lg, bias=False, rsf=1.0)
