@@ -44,7 +44,7 @@ STAGES = ("route", "permute", "gemm1_swiglu", "gemm2", "combine")
 # Kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (kStreamMaxRows, kBigRows,
 # kG2TileMaxRows; tests/test_bench.py checks they match the source)
 GEMM1_STREAM_MAX_ROWS = 1
-GEMM1_BIG_ROWS = 64
+GEMM1_BIG_ROWS = 16
 GEMM2_TILE_MAX_ROWS = 7
 
 

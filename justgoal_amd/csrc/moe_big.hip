@@ -804,6 +804,16 @@ constexpr int kB1Ns = 2;
 constexpr int kB1Wm = 2;
 constexpr int kB1Wn = 4;
 constexpr int kB1D = 3;
+// GEMM1 for 16..63 expected rows per expert: 64-row tiles (MS = 2, wave tile 32 rows x 32 C
+// columns; 40 KB of DMA per K step for 4.2 MFLOP per CU against 48 KB in the two 64-row
+// workgroups per CU of the LDS-tiled kernel), results bit-identical. Whole call against the
+// LDS-tiled GEMM1, two weight sets in rotation: DS-V3 T=512 211.3 -> 204.4 us, T=768 237.0 ->
+// 218.8, T=1024 249.8 -> 232.1, T=1536 309.9 -> 285.6, T=1792 343.7 -> 294.9; Qwen3-style T=256
+// 446.4 -> 427.9, T=512 485.5 -> 473.2, T=768 536.5 -> 517.9. Below 16 rows DS-V3 is slower on
+// them (T=256 171.1 against 187.9), and from 64 the 128-row tiles stay ahead (T=2048 301.8
+// against 307.7, T=4096 428.2 against 469.9).
+constexpr int kB1TallRows = 64;
+constexpr int kB1ShortMs = 2;
 constexpr int kB2Ms = 2;
 constexpr int kB2Ns = 4;
 constexpr int kB2Wm = 4;
@@ -822,18 +832,32 @@ constexpr int kB2ShortWn = 4;
 constexpr int kB2ShortNs = 2;
 constexpr int kB2ShortD = 4;
 
-hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
-                            const float* s13, const int32_t* counts, const int32_t* offsets,
-                            const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
-                            int max_pairs, hipStream_t stream) {
-  constexpr int BN = 16 * kB1Ns * kB1Wn;
-  if (I % BN != 0 || H / kBlock < kB1D - 1 || (int64_t)T * H >= kOutOfRange)
+template <int MS, int NS, int D, int WM, int WN>
+static hipError_t launch_gemm1_big_t(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
+                                     const float* s13, const int32_t* counts,
+                                     const int32_t* offsets, const int32_t* sorted_tok,
+                                     uint16_t* C, int T, int H, int I, int E_l, int max_pairs,
+                                     hipStream_t stream) {
+  constexpr int BN = 16 * NS * WN;
+  if (I % BN != 0 || H / kBlock < D - 1 || (int64_t)T * H >= kOutOfRange)
     return hipErrorNotSupported;
-  const int grid = big_grid(big_tiles(max_pairs, 16 * kB1Ms * kB1Wm, E_l) * (I / BN));
-  gemm1_big_kernel<kB1Ms, kB1Ns, kB1D, kB1Wm, kB1Wn><<<grid, (kB1Wm * kB1Wn + 1) * kWave, 0, stream>>>(
+  const int grid = big_grid(big_tiles(max_pairs, 16 * MS * WM, E_l) * (I / BN));
+  gemm1_big_kernel<MS, NS, D, WM, WN><<<grid, (WM * WN + 1) * kWave, 0, stream>>>(
       hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs,
       kSchedGemm1);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
+                            const float* s13, const int32_t* counts, const int32_t* offsets,
+                            const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
+                            int max_pairs, int rows_hint, hipStream_t stream) {
+  if (rows_hint < kB1TallRows)
+    return launch_gemm1_big_t<kB1ShortMs, kB1Ns, kB1D, kB1Wm, kB1Wn>(
+        hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs, stream);
+  return launch_gemm1_big_t<kB1Ms, kB1Ns, kB1D, kB1Wm, kB1Wn>(hs, hs_scale, w13, s13, counts,
+                                                              offsets, sorted_tok, C, T, H, I,
+                                                              E_l, max_pairs, stream);
 }
 
 template <int MS, int NS, int D, int WM, int WN>

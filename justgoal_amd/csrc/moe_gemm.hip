@@ -68,7 +68,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 
 // Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from sweeps
 // over DS-V3 T = 16..16384 and Qwen3-style T = 128..1024. GEMM1 streams weights up to 1 expected
-// row, uses the LDS-tiled kernels up to 63 and the large tiles from 64. GEMM2 uses the LDS-tiled
+// row, uses the LDS-tiled kernels up to 15 and the large-tile kernel from 16 (64-row tiles up to
+// 63, 128-row tiles from 64; moe_big.hip has the measurements). GEMM2 uses the LDS-tiled
 // kernel up to 7 expected rows (16-row tiles at <= 1, 32-row tiles above) and the large-tile
 // kernel from 8 (64-row tiles up to 63, 128-row tiles from 64); the streaming GEMM2 remains the
 // fallback for shapes the tiled kernel does not take.
@@ -83,19 +84,11 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 // T=128 432.3 -> 428.6, T=256 461.7 -> 452.2; at 6 rows the tiled kernel stays ahead (DS-V3 T=192
 // 163.5 against 168.3).
 constexpr int kStreamMaxRows = 1;
-constexpr int kBigRows = 64;
+constexpr int kBigRows = 16;
 constexpr int kG2TileMaxRows = 7;
-
-constexpr int kTileMt8Rows = 256;
 
 // M sub-tiles (of 16 rows) per work item for an expected segment length.
 static inline int stream_mt(int rows_hint) { return rows_hint <= 16 ? 1 : rows_hint <= 32 ? 2 : 4; }
-// LDS-tiled GEMM1 tile height: 32 rows up to 16 expected rows per expert (T=256: 122.8 ->
-// 116.7 us), 64 above (128-row tiles measured far slower at 32: 239 vs 158 us).
-constexpr int kTileMt2Rows = 16;
-static inline int tile_mt(int rows_hint) {
-  return rows_hint <= kTileMt2Rows ? 2 : rows_hint <= kTileMt8Rows ? 4 : 8;
-}
 
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                         const float* s13, const int32_t* counts, const int32_t* offsets,
@@ -107,11 +100,11 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, const uint8_t*
                                E_l, max_pairs, stream_mt(rows_hint), stream);
   if (rows_hint >= kBigRows) {
     const hipError_t b = launch_gemm1_big(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C,
-                                          T, H, I, E_l, max_pairs, stream);
+                                          T, H, I, E_l, max_pairs, rows_hint, stream);
     if (b != hipErrorNotSupported) return b;
   }
   const hipError_t e = launch_gemm1_tile(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C,
-                                         T, H, I, E_l, max_pairs, tile_mt(rows_hint), stream);
+                                         T, H, I, E_l, max_pairs, stream);
   if (e != hipErrorNotSupported) return e;
   return launch_gemm1_stream(hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l,
                              max_pairs, 4, stream);

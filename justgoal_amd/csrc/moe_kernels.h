@@ -62,7 +62,7 @@ hipError_t launch_gemm2_stream(const uint16_t* C, const uint8_t* w2, const float
 hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                             const float* s13, const int32_t* counts, const int32_t* offsets,
                             const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
-                            int max_pairs, hipStream_t stream);
+                            int max_pairs, int rows_hint, hipStream_t stream);
 hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s2,
                             const int32_t* counts, const int32_t* offsets, const float* sorted_w,
                             Gemm2Out dst, int H, int I, int E_l, int max_pairs, int rows_hint,
@@ -72,7 +72,7 @@ hipError_t launch_gemm2_big(const uint16_t* C, const uint8_t* w2, const float* s
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                              const float* s13, const int32_t* counts, const int32_t* offsets,
                              const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
-                             int max_pairs, int mt, hipStream_t stream);
+                             int max_pairs, hipStream_t stream);
 // LDS-tiled GEMM2 (mt = 16-row sub-tiles per workgroup tile).
 hipError_t launch_gemm2_tile(const uint16_t* C, const uint8_t* w2, const float* s2,
                              const int32_t* counts, const int32_t* offsets, const float* sorted_w,

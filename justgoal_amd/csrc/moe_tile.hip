@@ -1,5 +1,6 @@
-// LDS-tiled grouped GEMM1 + SwiGLU for segments of a few to tens of pairs per expert (GEMM2 of
-// that size runs on the large-tile kernels, whose padding-row skip measured faster).
+// LDS-tiled grouped GEMM1 + SwiGLU for segments of 2..15 expected pairs per expert (32-row
+// tiles; from 16 the large-tile kernel's 64-row tiles are faster), and the LDS-tiled GEMM2 for
+// segments of up to 7.
 //
 // A workgroup (4 waves) computes a BM x 64 tile of one expert's GEMM1 output (BM = 16*MT pairs).
 // Everything reaches LDS by DMA (buffer_load ... lds), so the only VGPRs spent on memory are the
@@ -510,7 +511,7 @@ constexpr int kG2tD = 4;
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
                              const float* s13, const int32_t* counts, const int32_t* offsets,
                              const int32_t* sorted_tok, uint16_t* C, int T, int H, int I, int E_l,
-                             int max_pairs, int mt, hipStream_t stream) {
+                             int max_pairs, hipStream_t stream) {
 #define JG_G1T(MT, D)                                                                           \
   {                                                                                             \
     if (H / kBlock < (D) - 1) return hipErrorNotSupported; /* lead must stay within one item */ \
@@ -522,9 +523,7 @@ hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uin
         hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs);       \
     return hipGetLastError();                                                                   \
   }
-  if (mt <= 2) JG_G1T(2, kG1tD)
-  if (mt <= 4) JG_G1T(4, kG1tD)
-  JG_G1T(8, (kG1tD > 4 ? 4 : kG1tD))  // a 128-row tile leaves room for 4 slots
+  JG_G1T(2, kG1tD)
 #undef JG_G1T
 }
 

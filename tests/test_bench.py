@@ -63,7 +63,8 @@ def test_kernel_family_thresholds_match_the_library_source():
     names = {n: bench.gemm1_kernel_name(c) for n, c in jin.CONFIGS.items()}
     assert names["ds_t16"] == "gemm1_stream_kernel"
     assert names["ds_t64"] == "gemm1_tile_kernel"
-    assert names["ds_t512"] == "gemm1_tile_kernel"
+    assert names["ds_t256"] == "gemm1_tile_kernel"
+    assert names["ds_t512"] == "gemm1_big_kernel"
     assert names["ds_t4096"] == "gemm1_big_kernel"
     g2names = {n: bench.gemm2_kernel_name(c) for n, c in jin.CONFIGS.items()}
     assert g2names["ds_t16"] == g2names["ds_t192"] == "gemm2_tile_kernel"

@@ -260,8 +260,8 @@ def test_definition_token_counts_via_reference_binding(gpu, T):
 
 # Qwen3 geometry (H=4096, I=1536: 12 K blocks in GEMM2) across the kernel families:
 # T * top_k / E = 0.06 and 0.5 stream weights in GEMM1 and use the LDS-tiled GEMM2 with 16-row
-# tiles, 4 uses the LDS-tiled GEMM1 and the LDS-tiled GEMM2 with 32-row tiles, ~19 the LDS-tiled
-# GEMM1 and the large-tile GEMM2.
+# tiles, 4 uses the LDS-tiled GEMM1 and the LDS-tiled GEMM2 with 32-row tiles, ~19 both
+# large-tile kernels with 64-row tiles.
 @pytest.mark.parametrize("T", [1, 8, 64, 300])
 def test_qwen3_small_and_mid_batches(gpu, T):
     say(f"qwen3 T={T}")
@@ -369,8 +369,9 @@ def boundary_counts(T, E=64, top_k=8):
                          ids=lambda v: getattr(v, "name", v))
 def test_segment_length_boundaries(gpu, geom, T):
     """Expert segments of exactly 1, 15, 16, 17, 31, 32, 33, ... pairs (and empty experts): the
-    tile edges of the LDS-tiled GEMM1 (T=128, 256), the large-tile kernels (T=512, 1024, and
-    GEMM2 from T=256), including large-tile waves whose rows of a tile are all padding; at
+    tile edges of the large-tile kernels' 64-row tiles (T=128, 256: 16 and 32 expected rows)
+    and 128-row tiles (T=512, 1024), including large-tile waves whose rows of a tile are all
+    padding, and of the LDS-tiled GEMM1's 32-row tiles (I=384, T=48 and 64); at
     I=384 the LDS-tiled GEMM2's 32-row tiles (T=48: 6 expected rows) and the large-tile GEMM2's
     64-row tiles in their 4-slot ring (T=64, 128, 256: 8, 16 and 32 expected rows; at I=256 that
     shape falls back to the 128-row tiles)."""
