@@ -264,7 +264,7 @@ def cpu_baseline(cfg, kw_dev, reps=3):
     return sec, torch.get_num_threads()
 
 
-DEFAULT_WORKLOADS = ("ds_t16", "ds_t64", "ds_t4096", "ds_t16384_skew", "qwen3_t1024")
+DEFAULT_WORKLOADS = ("ds_t16", "ds_t64", "ds_t1024", "ds_t4096", "ds_t16384_skew", "qwen3_t1024")
 
 
 def main():
