@@ -814,6 +814,19 @@ constexpr int kB1D = 3;
 // against 307.7, T=4096 428.2 against 469.9).
 constexpr int kB1TallRows = 64;
 constexpr int kB1ShortMs = 2;
+// 128-row tiles below 256 expected rows: 4 compute waves of 64 rows x 64 C columns (2 x 2; five
+// waves per workgroup, so up to 256 VGPRs each, and a quarter less LDS fragment traffic per K
+// step) instead of 8 of 64 x 32. Whole call against the 8-wave form, bit-identical: DS-V3
+// T=2048 302.7 -> 293.6 us, T=3072 379.3 -> 373.0, T=4096 436.1 -> 430.2, T=6144 565.5 ->
+// 555.1; Qwen3-style T=1024 551.2 -> 542.6. Where GEMM1 is MFMA-bound the 8-wave form, whose
+// two waves per SIMD overlap one's MFMAs with the other's scale FMAs, stays ahead (T=8192
+// 719.8 against 721.0 us, T=16384 skewed GEMM1 1947 against 2036 us). The same 2 x 2 layout for
+// the 64-row tiles measured within 1%, and for GEMM2 (2 x 2, or 4 x 1 waves of 32 x 128) 4-8%
+// slower at T=2048-16384.
+constexpr int kB1EightWaveRows = 256;
+constexpr int kB1WideNs = 4;
+constexpr int kB1WideWm = 2;
+constexpr int kB1WideWn = 2;
 constexpr int kB2Ms = 2;
 constexpr int kB2Ns = 4;
 constexpr int kB2Wm = 4;
@@ -854,6 +867,9 @@ hipError_t launch_gemm1_big(const uint8_t* hs, const float* hs_scale, const uint
                             int max_pairs, int rows_hint, hipStream_t stream) {
   if (rows_hint < kB1TallRows)
     return launch_gemm1_big_t<kB1ShortMs, kB1Ns, kB1D, kB1Wm, kB1Wn>(
+        hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs, stream);
+  if (rows_hint < kB1EightWaveRows)
+    return launch_gemm1_big_t<kB1Ms, kB1WideNs, kB1D, kB1WideWm, kB1WideWn>(
         hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs, stream);
   return launch_gemm1_big_t<kB1Ms, kB1Ns, kB1D, kB1Wm, kB1Wn>(hs, hs_scale, w13, s13, counts,
                                                               offsets, sorted_tok, C, T, H, I,
