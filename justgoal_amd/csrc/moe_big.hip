@@ -820,9 +820,9 @@ constexpr int kB1ShortMs = 2;
 // T=2048 302.7 -> 293.6 us, T=3072 379.3 -> 373.0, T=4096 436.1 -> 430.2, T=6144 565.5 ->
 // 555.1; Qwen3-style T=1024 551.2 -> 542.6. Where GEMM1 is MFMA-bound the 8-wave form, whose
 // two waves per SIMD overlap one's MFMAs with the other's scale FMAs, stays ahead (T=8192
-// 719.8 against 721.0 us, T=16384 skewed GEMM1 1947 against 2036 us). The same 2 x 2 layout for
-// the 64-row tiles measured within 1%, and for GEMM2 (2 x 2, or 4 x 1 waves of 32 x 128) 4-8%
-// slower at T=2048-16384.
+// 719.8 against 721.0 us, T=16384 skewed GEMM1 1947 against 2036 us). The same 2 x 2 layout
+// measured within 1% for the 64-row tiles of both GEMMs, and 4-8% slower for GEMM2's 128-row
+// tiles (2 x 2, or 4 x 1 waves of 32 x 128) at T=2048-16384.
 constexpr int kB1EightWaveRows = 256;
 constexpr int kB1WideNs = 4;
 constexpr int kB1WideWm = 2;
