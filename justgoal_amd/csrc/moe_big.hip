@@ -778,15 +778,25 @@ __global__ __launch_bounds__((WM * WN + 1) * kWave) void gemm2_big_kernel(
 
 }  // namespace
 
-// Item schedules (map_item). GEMM1: XCD-contiguous physical order over bands of 8 M-tiles,
-// N-tile-major inside a band, so an XCD's 32 concurrent items share W13 panels across up to 8
-// M-tiles and activation rows across 4 N-tiles. Against the tile-major round-robin order it cut
-// GEMM1's HBM fetch at T=4096 from 1.19 to 0.89 GB (algorithmic 0.80) and at T=16384 (skewed)
-// from 7.96 to 6.07 GB, and its time from 364 to 327 us for the Qwen3-style T=1024 batch
-// (T=4096: 222 -> 217 us; T=16384: within 1%). GEMM2 keeps the tile-major round-robin order:
-// every variant tried (XCD-contiguous, bands of 2-16) was 1-5% slower there.
+// Item schedules (map_item). The banded one: XCD-contiguous physical order over bands of 8
+// M-tiles, N-tile-major inside a band, so an XCD's 32 concurrent items share W13 panels across
+// up to 8 M-tiles and activation rows across 4 N-tiles. For GEMM1 it fetches fewer bytes than
+// the tile-major round-robin order (T=4096: 0.89 against 1.19 GB, algorithmic 0.80; T=16384
+// skewed: 6.07 against 7.96 GB) and made the Qwen3-style T=1024 batch's GEMM1 364 -> 327 us.
+// GEMM2 keeps the tile-major round-robin order: every variant tried (XCD-contiguous, bands of
+// 2-16) was 1-5% slower there.
 constexpr int kSchedGemm1 = 1 | (8 << 1);
 constexpr int kSchedGemm2 = 0;
+// Tile-major round-robin puts item i on XCD i % 8. When an expert has a multiple of 8 N-tiles,
+// each weight panel (expert, N-tile) then stays on one XCD for all of the expert's M-tiles, and
+// that order beats the banded XCD-contiguous one: DS-V3 GEMM1 (16 N-tiles) T=768 124.7 -> 123.0
+// us, T=1024 130.3 -> 125.1, T=1536 164.2 -> 158.5, T=2048 150.0 -> 141.3, T=3072 195.9 -> 182.1,
+// T=4096 204.5 -> 202.0, T=16384 skewed 1939 -> 1910. With 12 N-tiles (Qwen3-style GEMM1)
+// round-robin scatters each panel and each expert's activation rows over the XCDs and is 7-13%
+// slower (T=512 286 -> 324, T=1024 305 -> 345 us), so the banded order stays there. GEMM2 (56 or
+// 32 N-tiles) always has a multiple of 8.
+constexpr int kXcds = 8;
+constexpr int gemm1_sched(int n_tiles) { return n_tiles % kXcds == 0 ? 0 : kSchedGemm1; }
 
 static int big_grid(long long max_items) {
   const int cus = device_cu_count();
@@ -857,7 +867,7 @@ static hipError_t launch_gemm1_big_t(const uint8_t* hs, const float* hs_scale, c
   const int grid = big_grid(big_tiles(max_pairs, 16 * MS * WM, E_l) * (I / BN));
   gemm1_big_kernel<MS, NS, D, WM, WN><<<grid, (WM * WN + 1) * kWave, 0, stream>>>(
       hs, hs_scale, w13, s13, counts, offsets, sorted_tok, C, T, H, I, E_l, max_pairs,
-      kSchedGemm1);
+      gemm1_sched(I / BN));
   return hipGetLastError();
 }
 
