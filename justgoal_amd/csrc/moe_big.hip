@@ -824,16 +824,17 @@ constexpr int kB1D = 3;
 // against 307.7, T=4096 428.2 against 469.9).
 constexpr int kB1TallRows = 64;
 constexpr int kB1ShortMs = 2;
-// 128-row tiles below 256 expected rows: 4 compute waves of 64 rows x 64 C columns (2 x 2; five
+// 128-row tiles below 160 expected rows: 4 compute waves of 64 rows x 64 C columns (2 x 2; five
 // waves per workgroup, so up to 256 VGPRs each, and a quarter less LDS fragment traffic per K
-// step) instead of 8 of 64 x 32. Whole call against the 8-wave form, bit-identical: DS-V3
-// T=2048 302.7 -> 293.6 us, T=3072 379.3 -> 373.0, T=4096 436.1 -> 430.2, T=6144 565.5 ->
-// 555.1; Qwen3-style T=1024 551.2 -> 542.6. Where GEMM1 is MFMA-bound the 8-wave form, whose
-// two waves per SIMD overlap one's MFMAs with the other's scale FMAs, stays ahead (T=8192
-// 719.8 against 721.0 us, T=16384 skewed GEMM1 1947 against 2036 us). The same 2 x 2 layout
-// measured within 1% for the 64-row tiles of both GEMMs, and 4-8% slower for GEMM2's 128-row
-// tiles (2 x 2, or 4 x 1 waves of 32 x 128) at T=2048-16384.
-constexpr int kB1EightWaveRows = 256;
+// step) instead of 8 of 64 x 32. Bit-identical; GEMM1 stage against the 8-wave form, both on
+// the item order of gemm1_sched: DS-V3 T=2048 146.4 -> 142.0 us, T=3072 185.8 -> 182.9, T=4096
+// 202.9 -> 201.4; Qwen3-style T=1024 321 -> 307 (banded order), T=1536 334.3 -> 325.1, T=2048
+// 382.3 -> 371.0. From 160 rows, where GEMM1 turns MFMA-bound, the 8-wave form, whose two waves
+// per SIMD overlap one's MFMAs with the other's scale FMAs, is ahead: T=5120 235.2 against
+// 240.9, T=6144 248.7 against 256.6, T=8192 334.5 against 341.3, T=16384 skewed 1922 against
+// 2006. The same 2 x 2 layout measured within 1% for the 64-row tiles of both GEMMs, and 4-8%
+// slower for GEMM2's 128-row tiles (2 x 2, or 4 x 1 waves of 32 x 128) at T=2048-16384.
+constexpr int kB1EightWaveRows = 160;
 constexpr int kB1WideNs = 4;
 constexpr int kB1WideWm = 2;
 constexpr int kB1WideWn = 2;

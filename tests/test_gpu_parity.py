@@ -372,7 +372,8 @@ def test_segment_length_boundaries(gpu, geom, T):
     """Expert segments of exactly 1, 15, 16, 17, 31, 32, 33, ... pairs (and empty experts): the
     tile edges of the large-tile kernels' 64-row tiles (T=128, 256: 16 and 32 expected rows)
     and 128-row tiles (T=512, 1024 with GEMM1's 4-wave layout, T=2048 with its 8-wave one:
-    64, 128 and 256 expected rows), including large-tile waves whose rows of a tile are all
+    64, 128 and 256 expected rows; with 2 or 3 N-tiles GEMM1 takes its banded item order, the
+    DS-V3 cases its round-robin one), including large-tile waves whose rows of a tile are all
     padding, and of the LDS-tiled GEMM1's 32-row tiles (I=384, T=48 and 64); at
     I=384 the LDS-tiled GEMM2's 32-row tiles (T=48: 6 expected rows) and the large-tile GEMM2's
     64-row tiles in their 4-slot ring (T=64, 128, 256: 8, 16 and 32 expected rows; at I=256 that
