@@ -92,7 +92,7 @@ int64_t moe_workspace_bytes_ex(const moe_geometry* geom, int T);
  * MOE_NOALLOC_SCRATCH_BYTES in the library's device code, one per GPU, held until the process
  * ends (its device address is looked up once per device on the first call there). A call whose
  * moe_workspace_bytes_ex exceeds that size returns MOE_ERR_SCRATCH_SIZE before enqueueing
- * anything (DS-V3: up to 503 tokens; the Qwen3-style geometry: up to 816). Every call on a GPU
+ * anything (DS-V3: up to 503 tokens; the Qwen3-style geometry: up to 815). Every call on a GPU
  * shares that GPU's array: calls that overlap in time on one GPU (other streams, other host
  * threads) race and must not be issued; calls ordered on one stream are fine.
  */
@@ -124,7 +124,7 @@ enum {
   MOE_WS_PARTIAL,        /* bf16  [T * (k - 1), H]  weighted GEMM2 rows of each token's 2nd..k-th
                             local pair (k = min(top_k, E_l)); the 1st goes straight into `out` */
   MOE_WS_CHUNK_COUNTS,   /* int32 [ceil(T/c), E_l] pairs per local expert per c-token group,
-                            c = 4 for T <= 256, else 16 (one row per routing workgroup) */
+                            c = 4 for T <= 2048, else 16 (one row per routing workgroup) */
   MOE_WS_PAIR_DST,       /* int32 [Npmax]     GEMM2 destination of each pair: t (row of out) for
                             a token's first local pair, else -1 - (t * (k - 1) + j - 1) for its
                             (j+1)-th (row of partial) */

@@ -22,7 +22,7 @@ hipError_t launch_permute(const int32_t* topk_idx, const float* topk_w, const in
                           int32_t* offsets, int32_t* sorted_tok, float* sorted_w,
                           int32_t* pair_dst, int32_t* pair_of, hipStream_t stream);
 
-// Number of routing workgroups (4 tokens each up to T = 256, 16 above) = rows of the chunk count
+// Number of routing workgroups (4 tokens each up to T = 2048, 16 above) = rows of the chunk count
 // table.
 int route_chunks(int T);
 

@@ -1,6 +1,6 @@
 // Routing and token-permute kernels.
 //
-// route_kernel: one wave64 per token (4 tokens per workgroup up to T = 256, 16 above), each
+// route_kernel: one wave64 per token (4 tokens per workgroup up to T = 2048, 16 above), each
 //   lane owning VPL = E/64 consecutive experts.
 //   DeepSeek no-aux routing (reference semantics: goal_full_shape/fable-5.1/moe_fp8_fwd/MOEDIR/
 //   moe_common.cuh:271-365, kda05_reproduction_single_shape/fable-5.1/moe_fp8_fwd/t14107/
@@ -26,10 +26,12 @@ namespace jgmoe {
 namespace {
 
 constexpr int kRouteWaves = 16;          // most tokens per routing workgroup (one wave each)
-// Routing is VALU-latency-bound (sigmoid, DPP top-k chains): small batches use 4-token
-// workgroups so their tokens spread over more CUs; larger ones keep 16 per workgroup so the
-// permute kernel has fewer count rows to sum.
-constexpr int kRouteSmallT = 256, kRouteWavesSmall = 4;
+// Routing is VALU-latency-bound (sigmoid, DPP top-k chains): batches up to 2048 tokens use
+// 4-token workgroups so their tokens spread over more CUs; larger ones keep 16 per workgroup so
+// the permute kernel has fewer count rows to sum. Against a switch at 256 tokens, route +
+// permute stage time: DS-V3 T=512 19.5 -> 16.8 us, T=1024 20.3 -> 17.6, T=2048 21.3 -> 20.1; at
+// T=4096 the longer permute cancels the faster routing (22.9 against 24.1 us).
+constexpr int kRouteSmallT = 2048, kRouteWavesSmall = 4;
 __host__ __device__ __forceinline__ int route_tokens_per_group(int T) {
   return T <= kRouteSmallT ? kRouteWavesSmall : kRouteWaves;
 }

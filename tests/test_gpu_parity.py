@@ -436,9 +436,9 @@ def test_workspace_per_stream_grows_and_is_not_shared(gpu):
     release_workspaces()
 
 
-# Routing workgroups hold 4 tokens up to T=256 and 16 above: both sides of the switch and ragged
-# counts around it (permute then sums 64 or 17 count rows).
-@pytest.mark.parametrize("T", [4, 255, 256, 257, 513])
+# Routing workgroups hold 4 tokens up to T=2048 and 16 above: both sides of the switch and ragged
+# counts around it (permute then sums 512 or 129 count rows).
+@pytest.mark.parametrize("T", [4, 255, 257, 2047, 2048, 2049, 2561])
 def test_route_group_boundary(gpu, T):
     check_case(MINI_DS, T, gpu, seed=T + 1)
 
@@ -515,7 +515,7 @@ def test_random_geometries(gpu, case):
 # The routing-only entry point (moe_route_ex) on its own, at the model geometries: both routing
 # methods, a ragged T on each side of the routing workgroup switch, a full-size batch, and an EP
 # rank's expert window; every returned region is compared bit for bit with the oracle.
-@pytest.mark.parametrize("geom,T,off", [(DS_V3, 1, 0), (DS_V3, 257, 32), (DS_V3, 4096, 224),
+@pytest.mark.parametrize("geom,T,off", [(DS_V3, 1, 0), (DS_V3, 2049, 32), (DS_V3, 4096, 224),
                                         (QWEN3, 3, 0), (QWEN3, 1000, 0), (QWEN3, 4096, 0)])
 def test_route_entry_matches_oracle(gpu, geom, T, off):
     from justgoal_amd.moe import route
