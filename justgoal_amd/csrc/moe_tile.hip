@@ -506,6 +506,8 @@ static inline long long tile_count(int max_pairs, int bm, int E_l) {
 constexpr int kG1tD = 3;
 // GEMM2's K blocks are half as many bytes of weight per step (bf16 C is the larger operand), so
 // four slots still fit two workgroups per CU; D = 4 measured ahead of D = 3 at 2..8 rows/expert.
+// 16-row tiles with deeper rings (the freed C space) were slower at 0.5-6 expected rows: D = 5
+// and 6 by 1-4% (DS-V3 T=64 126.1 -> 127.9 / 128.2 us), D = 8, one workgroup per CU, by 6-27%.
 constexpr int kG2tD = 4;
 
 hipError_t launch_gemm1_tile(const uint8_t* hs, const float* hs_scale, const uint8_t* w13,
