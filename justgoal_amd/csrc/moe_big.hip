@@ -1,10 +1,13 @@
-// Large-tile grouped GEMMs for long per-expert segments (prefill-sized and skewed batches; GEMM2
-// also for a few pairs per expert, where its padding-row skip keeps part-filled tiles cheap).
+// Large-tile grouped GEMMs for longer per-expert segments (GEMM1 from 16 expected pairs per
+// expert, GEMM2 from 8; GEMM2's padding-row skip keeps part-filled tiles cheap).
 //
-// A workgroup (one per CU) computes a 128 x 128 output tile of one expert with eight compute
-// waves (GEMM1: 2x4 grid, wave tile 64 rows x 32 C columns; GEMM2: 4x2, 32 rows x 64 H columns)
-// and one producer wave. Both operands reach LDS by DMA into a 3-slot ring, so every weight
-// K-block is fetched once per 128 rows and every activation K-block once per 128 columns:
+// A workgroup (one per CU) computes a 128-row x 128-column output tile of one expert with eight
+// compute waves (GEMM1: 2x4 grid, wave tile 64 rows x 32 C columns; GEMM2: 4x2, 32 rows x 64 H
+// columns) and one producer wave. Both operands reach LDS by DMA into a 3-slot ring, so every
+// weight K-block is fetched once per 128 rows and every activation K-block once per 128
+// columns. The same kernels are instantiated with 64-row tiles for shorter segments (2x4 waves
+// of 32 x 32; GEMM2 then has room for a 4-slot ring) and, for GEMM1 from 64 to 159 expected
+// rows, with four compute waves of 64 x 64; the launchers below pick the form:
 //
 // * GEMM1: 128 rows of fp8 hidden states (gathered through the pair -> token list) plus their
 //   activation scales, and 128 columns of C, i.e. 128 X1 rows and 128 X2 rows of W13. The
@@ -843,7 +846,7 @@ constexpr int kB2Ns = 4;
 constexpr int kB2Wm = 4;
 constexpr int kB2Wn = 2;
 constexpr int kB2D = 3;
-// GEMM2 for 17..63 expected rows per expert: 64-row tiles (2 x 4 waves of 32 x 32, NS = 2) in a
+// GEMM2 for 8..63 expected rows per expert: 64-row tiles (2 x 4 waves of 32 x 32, NS = 2) in a
 // 4-slot ring (146 KB of LDS). Against the 128-row tiles, whole call, two weight sets in
 // rotation, results bit-identical: DS-V3 T=768 252.1 -> 236.6 us, T=1024 260.6 -> 249.8,
 // T=1280 283.0 -> 275.4, T=1536 310.0 -> 306.9, T=1792 344.1 -> 339.9; Qwen3-style T=512 503.3 ->
