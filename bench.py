@@ -15,8 +15,10 @@ Prints ONE JSON line. ``value`` is TFLOP/s of the headline workload over algorit
 (6*H*I per local (token, expert) pair, pairs counted from the routing of the run). Each workload
 carries a ``roofline`` block for its dominant kernel (the stage with the largest time, from
 events the library records on the operator's stream); the top-level ``roofline`` is the
-headline's. ``cpu_baseline`` times the CPU oracle (the dequantise-then-fp32 PyTorch-CPU
-restatement of the operator) on all host cores.
+headline's. Every workload also carries a ``cpu_baseline``: the CPU oracle (the
+dequantise-then-fp32 PyTorch-CPU restatement of the operator) timed on all host cores on the same
+inputs (median of 3; a single call for the skewed T=16384 batch); the top-level one is the
+headline's.
 """
 from __future__ import annotations
 
@@ -245,15 +247,30 @@ def load_traffic(stage, name):
         return json.load(f).get("bytes_per_launch")
 
 
-def cpu_baseline(cfg, kw_dev, reps=3):
-    """The CPU oracle on all of this host's cores, on the full headline workload (median of
-    ``reps`` after one warm-up)."""
+# CPU-baseline repetitions per workload: median of 3 (one warm-up call first for the small
+# batches), and a single call for the skewed T=16384 batch, whose oracle call alone takes about a
+# minute on 16 host threads.
+CPU_BASELINE_REPS = {"ds_t16384_skew": (1, 0)}
+CPU_BASELINE_DEFAULT = (3, 1)
+CPU_BASELINE_BIG = (3, 0)  # batches whose oracle call takes seconds: no separate warm-up
+
+
+def cpu_baseline(cfg, kw_dev, cpu_weights, flops):
+    """The CPU oracle (torch-CPU fp32 dequantise-then-matmul restatement of the operator) on all
+    of this host's cores, on the full workload with the same inputs as the GPU run (weight set 0,
+    already on the host). Returns the bench line's ``cpu_baseline`` object."""
     import oracle
     cores = max(1, os.cpu_count() or 1)
     torch.set_num_threads(cores)
     kw = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in kw_dev.items()}
+    kw.update(gemm1_weights=cpu_weights[0], gemm1_weights_scale=cpu_weights[1],
+              gemm2_weights=cpu_weights[2], gemm2_weights_scale=cpu_weights[3])
     geom = cfg.geom
-    oracle.moe_reference(kw, geom)  # warm-up
+    reps, warm = CPU_BASELINE_REPS.get(
+        cfg.name, CPU_BASELINE_BIG if cfg.tokens >= 4096 or geom.local_experts > 32
+        else CPU_BASELINE_DEFAULT)
+    for _ in range(warm):
+        oracle.moe_reference(kw, geom)
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -261,7 +278,13 @@ def cpu_baseline(cfg, kw_dev, reps=3):
         ts.append(time.perf_counter() - t0)
     ts.sort()
     sec = ts[len(ts) // 2]
-    return sec, torch.get_num_threads()
+    what = f"median of {reps}" if reps > 1 else "one call"
+    if warm:
+        what += f" after {warm} warm-up"
+    return {"value": flops / sec / 1e12, "unit": "TFLOPS", "cores": torch.get_num_threads(),
+            "kind": "port", "ms_per_call": sec * 1e3,
+            "sample": f"full {cfg.name} call (T={cfg.tokens}), {what}, torch-CPU fp32 "
+                      "dequantise-then-matmul oracle, weight set 0"}
 
 
 DEFAULT_WORKLOADS = ("ds_t16", "ds_t64", "ds_t1024", "ds_t4096", "ds_t16384_skew", "qwen3_t1024")
@@ -311,14 +334,16 @@ def main():
     names = [n for n in args.workloads.split(",") if n]
     if args.config not in names:
         names.insert(0, args.config)
-    results, head, head_kw = {}, None, None
+    results, head = {}, None
     weights = {}
     # group by geometry so each weight set is generated and resident once
     for geom in dict.fromkeys(jin.CONFIGS[n].geom for n in names):
         t0 = time.time()
         log(f"[bench] generating {geom.name} weights")
-        wts = [tuple(t.to(dev) for t in jin.make_weights(geom, seed=k))
-               for k in range(args.weight_sets)]
+        wts_cpu = [jin.make_weights(geom, seed=k) for k in range(args.weight_sets)]
+        wts = [tuple(t.to(dev) for t in w) for w in wts_cpu]
+        cpu_w0 = wts_cpu[0]
+        del wts_cpu
         log(f"[bench] weights ready in {time.time() - t0:.1f}s")
         for n in names:
             cfg = jin.CONFIGS[n]
@@ -330,27 +355,24 @@ def main():
                 f"{r['tflops']:.1f} TFLOPS, {r['gb_s']:.0f} GB/s, floor frac "
                 f"{r['call_floor_frac']:.3f}; {rl['kernel']} {rl['frac']:.3f} of {rl['bound']}; "
                 f"stages " + ", ".join(f"{k} {v * 1e3:.1f}us" for k, v in r["stage_ms"].items()))
+            if not args.no_cpu_baseline:
+                t1 = time.time()
+                r["cpu_baseline"] = cpu_baseline(cfg, kw, cpu_w0, r["algorithmic_flops"])
+                r["gpu_speedup_vs_cpu"] = r["cpu_baseline"]["ms_per_call"] / r["ms_per_call"]
+                log(f"[bench] {n}: CPU oracle {r['cpu_baseline']['ms_per_call']:.1f} ms/call on "
+                    f"{r['cpu_baseline']['cores']} threads ({time.time() - t1:.0f}s)")
             results[n] = r
             if n == args.config:
-                head, head_kw = r, kw
-            else:
-                del kw
-        del wts
+                head = r
+            del kw
+        del wts, cpu_w0
         torch.cuda.empty_cache()
     quant = [] if args.no_quant else [
         measure_quant(T, head_cfg.geom.hidden, steps, args.warmup, dev) for T in (4096, 64)]
     for r in quant:
         log(f"[bench] activation quant T={r['tokens']}: {r['ms_per_call'] * 1e3:.1f} us, "
             f"{r['gb_s']:.0f} GB/s")
-    cpu = None
-    if not args.no_cpu_baseline:
-        log("[bench] timing the CPU oracle")
-        sec, cores = cpu_baseline(head_cfg, head_kw)
-        cpu = {"value": head["algorithmic_flops"] / sec / 1e12, "unit": "TFLOPS", "cores": cores,
-               "kind": "port", "ms_per_call": sec * 1e3,
-               "sample": f"full {head_cfg.name} call (T={head_cfg.tokens}, {head['pairs']} local "
-                         "pairs), median of 3 after 1 warm-up, torch-CPU fp32 "
-                         "dequantise-then-matmul"}
+    cpu = head.get("cpu_baseline")
     out = {
         "metric": METRIC, "value": head["tflops"], "unit": "TFLOPS", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": head["ms_per_call"],

@@ -49,6 +49,18 @@ def test_noalloc_matches_workspace_entry(gpu, geom, sizes):
         print(f"noalloc: {geom.name} call {i} T={T}", flush=True)
         got, ref = _both(geom, w, T, seed=40 + i, dev=gpu)
         assert torch.equal(got, ref), f"call {i} (T={T}) differs from moe_run_ex"
+    # the entry point's contract: a call allocates no device memory (free bytes unchanged around
+    # a call whose inputs and output already exist)
+    L = _lib.lib()
+    T = sizes[-1]
+    act = {k: v.to(gpu) for k, v in jin.make_activations(geom, T, seed=7).items()}
+    out = torch.empty((T, geom.hidden), dtype=torch.bfloat16, device=gpu)
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(gpu)[0]
+    assert L.moe_run_noalloc(*_args(geom, w, act, out), T, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(gpu)[0] == free0, "moe_run_noalloc changed free device memory"
     del w
 
 
