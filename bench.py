@@ -148,9 +148,18 @@ def roofline_block(stage, kernel, ms, flops, nbytes, peak_tflops, workload):
         bound, achieved, peak, unit = "mfma", flops / (ms * 1e-3) / 1e12, peak_tflops, "TFLOP/s"
     else:
         bound, achieved, peak, unit = "hbm", nbytes / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
-    return {"bound": bound, "kernel": kernel, "stage": stage, "achieved": achieved, "peak": peak,
-            "unit": unit, "frac": achieved / peak, "traffic": load_traffic(stage, workload),
-            "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "avg_launch_ms": ms}
+    blk = {"bound": bound, "kernel": kernel, "stage": stage, "achieved": achieved, "peak": peak,
+           "unit": unit, "frac": achieved / peak, "traffic": load_traffic(stage, workload),
+           "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "avg_launch_ms": ms}
+    # The same figure from the committed rocprofv3 kernel trace of this bench (its average
+    # duration for this kernel and workload), so the event-timed frac can be checked against it.
+    us = load_rocprof_avg_us(kernel, workload)
+    if us is not None:
+        r_ms = us * 1e-3
+        blk["rocprof_avg_launch_ms"] = r_ms
+        blk["frac_rocprof"] = ((flops / (r_ms * 1e-3) / 1e12) if bound == "mfma"
+                               else (nbytes / (r_ms * 1e-3) / 1e9)) / peak
+    return blk
 
 
 def measure(cfg, weight_sets, steps, warmup, settle_ms, dev, seed=None):
@@ -245,6 +254,17 @@ def load_traffic(stage, name):
         return None
     with open(p) as f:
         return json.load(f).get("bytes_per_launch")
+
+
+def load_rocprof_avg_us(kernel, name):
+    """Average duration (us) of ``kernel`` in ``name``'s calls in the committed rocprofv3
+    --kernel-trace summary of this bench, if present."""
+    p = os.path.join(HERE, "profiles", "kernel_avg_us.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        ent = json.load(f).get("workloads", {}).get(name, {}).get(kernel)
+    return None if ent is None else ent["average_us"]
 
 
 # CPU-baseline repetitions per workload: median of 3 (one warm-up call first for the small
