@@ -18,11 +18,11 @@
 // block maxima (subnormal to largest finite), 1.35e8 pairs; the kernel's own test runs every
 // finite bf16 value under 48 block maxima against the CPU oracle's division.
 //
-// HBM-bound (3 bytes per element plus 4 per 128 elements). A workgroup owns 16 tokens x 512
-// columns: each wave quantises one token's 512 columns per pass (lane = 8 columns of one block;
+// HBM-bound (3 bytes per element plus 4 per 128 elements). A workgroup owns 16 (or 4) tokens x
+// 512 columns: each wave quantises one token's 512 columns per pass (lane = 8 columns of one block;
 // the block amax is a 16-lane xor reduction), so loads are 1 KiB and code stores 512 B per wave
-// instruction; the workgroup's 64 scales leave through LDS as four 64-byte rows of the
-// transposed scale matrix.
+// instruction; the workgroup's scales leave through LDS as four rows (one per block, 64 or 16
+// bytes) of the transposed scale matrix.
 #include "moe_device.h"
 #include "moe_kernels.h"
 
@@ -30,8 +30,16 @@ namespace jgmoe {
 
 namespace {
 
-constexpr int kQTok = 16;    // tokens per workgroup
 constexpr int kQBlk = 4;     // 128-column blocks per workgroup (512 columns)
+// Tokens per workgroup. 16 (four per wave, one after another) for large batches; up to 1024
+// tokens, 4 (one per wave), so a small batch spreads over four times the workgroups and each
+// wave waits on one load instead of four. Kernel time per launch in a replayed graph (DS-V3
+// H = 7168): T=16 3.8 -> 2.3 us, T=64 3.8 -> 2.4, T=256 4.0 -> 3.0, T=1024 6.0 -> 5.7; at
+// T=16384 the 4-token form is slower (80 against 74 us). Loading a wave's four rows up front
+// in the 16-token form took T=4096 from 16.1 to 17.5 us.
+constexpr int kQTok = 16;
+constexpr int kQTokSmall = 4;
+constexpr int kQSmallT = 1024;
 constexpr int kQWaves = 4;
 
 // Four fp32 -> four e4m3 bytes (OCP e4m3fn on gfx950), round to nearest even. Inputs are
@@ -42,17 +50,19 @@ __device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, flo
   return (uint32_t)v;
 }
 
+template <int TOK>
 __global__ __launch_bounds__(kQWaves * kWave) void quant_act_kernel(
     const uint16_t* __restrict__ x, int T, int H, uint8_t* __restrict__ q,
     float* __restrict__ scale) {
-  __shared__ float sc[kQBlk][kQTok];
+  static_assert(TOK % kQWaves == 0 && kQBlk * TOK <= kWave, "one scale per lane of wave 0");
+  __shared__ float sc[kQBlk][TOK];
   const int lane = threadIdx.x & (kWave - 1), w = wave_id();
   const int NB = H / kBlock;
-  const int t0 = blockIdx.x * kQTok, b0 = blockIdx.y * kQBlk;
+  const int t0 = blockIdx.x * TOK, b0 = blockIdx.y * kQBlk;
   const int blk = b0 + (lane >> 4);  // this lane's 128-column block
   const bool active = blk < NB;
   const int col = blk * kBlock + 8 * (lane & 15);
-  for (int j = w; j < kQTok; j += kQWaves) {
+  for (int j = w; j < TOK; j += kQWaves) {
     const int t = t0 + j;  // wave-uniform
     float v[8];
     float amax = 0.f;
@@ -91,9 +101,9 @@ __global__ __launch_bounds__(kQWaves * kWave) void quant_act_kernel(
     if ((lane & 15) == 0) sc[lane >> 4][j] = cs;
   }
   __syncthreads();
-  if (w == 0) {
-    const int b = b0 + (lane >> 4), t = t0 + (lane & 15);
-    if (b < NB && t < T) scale[(size_t)b * T + t] = sc[lane >> 4][lane & 15];
+  if (w == 0 && lane < kQBlk * TOK) {
+    const int b = b0 + lane / TOK, t = t0 + lane % TOK;
+    if (b < NB && t < T) scale[(size_t)b * T + t] = sc[lane / TOK][lane % TOK];
   }
 }
 
@@ -102,8 +112,13 @@ __global__ __launch_bounds__(kQWaves * kWave) void quant_act_kernel(
 hipError_t launch_quantize_activations(const uint16_t* x, int T, int H, uint8_t* q, float* scale,
                                        hipStream_t stream) {
   const int NB = H / kBlock;
+  if (T <= kQSmallT) {
+    const dim3 grid((T + kQTokSmall - 1) / kQTokSmall, (NB + kQBlk - 1) / kQBlk);
+    quant_act_kernel<kQTokSmall><<<grid, kQWaves * kWave, 0, stream>>>(x, T, H, q, scale);
+    return hipGetLastError();
+  }
   const dim3 grid((T + kQTok - 1) / kQTok, (NB + kQBlk - 1) / kQBlk);
-  quant_act_kernel<<<grid, kQWaves * kWave, 0, stream>>>(x, T, H, q, scale);
+  quant_act_kernel<kQTok><<<grid, kQWaves * kWave, 0, stream>>>(x, T, H, q, scale);
   return hipGetLastError();
 }
 

@@ -2,7 +2,8 @@
 oracle: e4m3 codes and fp32 scales bit-exact. Cases: random rows with edge blocks (all-zero,
 values in the e4m3 subnormal range, exact rounding ties, a huge dynamic range), every finite
 bf16 value under each of 48 block maxima (subnormal to largest finite), ragged shapes
-(T not a multiple of 16, H not a multiple of 512), the full DS-V3 T=4096 batch, and the chain
+(T not a multiple of 16 or 4, on both sides of the 1024-token switch between 4- and 16-token
+workgroups; H not a multiple of 512), the full DS-V3 T=4096 batch, and the chain
 quantise -> operator against the oracle on the same bf16 input.
 """
 import sys
@@ -99,7 +100,8 @@ def test_every_bf16_value_under_each_amax(gpu):
     check(every_value_blocks(amaxes), gpu)
 
 
-@pytest.mark.parametrize("T,H", [(1, 128), (17, 384), (33, 640), (5, 4096)])
+@pytest.mark.parametrize("T,H", [(1, 128), (17, 384), (33, 640), (5, 4096),
+                                 (1023, 384), (1024, 640), (1025, 384), (1030, 640)])
 def test_ragged_shapes(gpu, T, H):
     x = (torch.randn(T, H, generator=torch.Generator().manual_seed(T * H)) * 3).bfloat16()
     check(x, gpu)
