@@ -45,7 +45,7 @@ PEAK_BF16_TFLOPS = 2500.0
 STAGES = ("route", "permute", "gemm1_swiglu", "gemm2", "combine")
 # Kernel-family thresholds of justgoal_amd/csrc/moe_gemm.hip (kStreamMaxRows, kBigRows,
 # kG2TileMaxRows; tests/test_bench.py checks they match the source)
-GEMM1_STREAM_MAX_ROWS = 1
+GEMM1_STREAM_MAX_ROWS = 4
 GEMM1_BIG_ROWS = 16
 GEMM2_TILE_MAX_ROWS = 7
 

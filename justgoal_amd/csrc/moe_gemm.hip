@@ -67,8 +67,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 }
 
 // Kernel families by rows_hint = T*top_k/E (expected pairs per expert), per GEMM, from sweeps
-// over DS-V3 T = 16..16384 and Qwen3-style T = 128..1024. GEMM1 streams weights up to 1 expected
-// row, uses the LDS-tiled kernels up to 15 and the large-tile kernel from 16 (64-row tiles up to
+// over DS-V3 T = 16..16384 and Qwen3-style T = 32..1024. GEMM1 streams weights up to 4 expected
+// rows, uses the LDS-tiled kernels up to 15 and the large-tile kernel from 16 (64-row tiles up to
 // 63, 128-row tiles from 64; moe_big.hip has the measurements). GEMM2 uses the LDS-tiled
 // kernel up to 7 expected rows (16-row tiles at <= 1, 32-row tiles above) and the large-tile
 // kernel from 8 (64-row tiles up to 63, 128-row tiles from 64); the streaming GEMM2 remains the
@@ -83,7 +83,13 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 // T=256 (8 rows) 172.2 -> 170.4 us, T=384 186.1 -> 178.9, T=512 226.4 -> 210.0; Qwen3-style
 // T=128 432.3 -> 428.6, T=256 461.7 -> 452.2; at 6 rows the tiled kernel stays ahead (DS-V3 T=192
 // 163.5 against 168.3).
-constexpr int kStreamMaxRows = 1;
+// Since the streaming GEMM1 deals its items wave-index major (every CU busy when a batch has
+// fewer items than the grid has waves), it beats the LDS-tiled GEMM1 up to 4 expected rows
+// (whole call, DS-V3: T=64 126.7 -> 125.6 us, T=96 157.9 -> 151.4, T=128 158.3 -> 152.6;
+// Qwen3-style T=32 367.2 -> 358.1, T=64 416.5 -> 405.3); level at 5 (DS-V3 T=160, Qwen3 T=80)
+// and behind from 6 (DS-V3 T=176 162.9 against 166.8, T=192 164.2 against 172.6, Qwen3 T=96
+// 425.5 against 428.2, T=128 427.4 against 438.5).
+constexpr int kStreamMaxRows = 4;
 constexpr int kBigRows = 16;
 constexpr int kG2TileMaxRows = 7;
 

@@ -62,7 +62,7 @@ def test_kernel_family_thresholds_match_the_library_source():
     from justgoal_amd import inputs as jin
     names = {n: bench.gemm1_kernel_name(c) for n, c in jin.CONFIGS.items()}
     assert names["ds_t16"] == "gemm1_stream_kernel"
-    assert names["ds_t64"] == "gemm1_tile_kernel"
+    assert names["ds_t64"] == "gemm1_stream_kernel"
     assert names["ds_t256"] == "gemm1_tile_kernel"
     assert names["ds_t512"] == "gemm1_big_kernel"
     assert names["ds_t4096"] == "gemm1_big_kernel"

@@ -260,9 +260,9 @@ def test_definition_token_counts_via_reference_binding(gpu, T):
 
 # Qwen3 geometry (H=4096, I=1536: 12 K blocks in GEMM2) across the kernel families:
 # T * top_k / E = 0.06 and 0.5 stream weights in GEMM1 and use the LDS-tiled GEMM2 with 16-row
-# tiles, 4 uses the LDS-tiled GEMM1 and the LDS-tiled GEMM2 with 32-row tiles, ~19 both
-# large-tile kernels with 64-row tiles.
-@pytest.mark.parametrize("T", [1, 8, 64, 300])
+# tiles, 4 streams GEMM1 and uses the LDS-tiled GEMM2 with 32-row tiles, 8 the LDS-tiled GEMM1
+# and the large-tile GEMM2 with 64-row tiles, ~19 both large-tile kernels with 64-row tiles.
+@pytest.mark.parametrize("T", [1, 8, 64, 128, 300])
 def test_qwen3_small_and_mid_batches(gpu, T):
     say(f"qwen3 T={T}")
     check_case(QWEN3, T, gpu, seed=T + 11, tokens_checked=min(T, 64))
@@ -390,14 +390,16 @@ SEG_WIDE = Geometry(256, 256, 256, 256, 8, 1, 1, ROUTING_SOFTMAX, "segments-wide
 SEG_WIDE_G2T = Geometry(256, 384, 256, 256, 8, 1, 1, ROUTING_SOFTMAX, "segments-wide-i384")
 
 
-@pytest.mark.parametrize("geom", [SEG_WIDE, SEG_WIDE_G2T], ids=lambda g: g.name)
-def test_segment_length_boundaries_streaming(gpu, geom):
+@pytest.mark.parametrize("geom,T", [(SEG_WIDE, 32), (SEG_WIDE_G2T, 32), (SEG_WIDE, 128)],
+                         ids=lambda v: getattr(v, "name", v))
+def test_segment_length_boundaries_streaming(gpu, geom, T):
     """T * top_k / E = 1 on expert segments of 0, 1, 2, 15, 16, 17, 31 and 32 pairs: the edges
     of the 16-row items of the streaming kernels (both GEMMs at I=256) and of the LDS-tiled
-    GEMM2's 16-row tiles (I=384), one and two items per segment."""
-    T = 32
+    GEMM2's 16-row tiles (I=384), one and two items per segment; T * top_k / E = 4 (the most
+    expected rows the streaming GEMM1 takes) on segments of up to 97 pairs, seven items."""
     counts = boundary_counts(T, E=geom.num_experts)
     assert {15, 16, 17, 31, 32} <= set(counts)
+    assert T < 128 or {63, 64, 65, 95, 96, 97} <= set(counts)
     lg = logits_for_counts(counts, T, geom.num_experts)
     _, ws = check_case(geom, T, gpu, seed=10, logits=lg, bias=False, rsf=1.0)
     assert ws["counts"].cpu().tolist() == counts
