@@ -288,8 +288,8 @@ def load_rocprof_avg_us(kernel, name):
 
 
 # CPU-baseline repetitions per workload: median of 3 (one warm-up call first for the small
-# batches), and a single call for the skewed T=16384 batch, whose oracle call alone takes about a
-# minute on 16 host threads.
+# batches), and a single call for the skewed T=16384 batch (about 5 s per oracle call on the GPU
+# host's 16 threads, minutes on a few cores). The six baselines add ~25 s to a default run.
 CPU_BASELINE_REPS = {"ds_t16384_skew": (1, 0)}
 CPU_BASELINE_DEFAULT = (3, 1)
 CPU_BASELINE_BIG = (3, 0)  # batches whose oracle call takes seconds: no separate warm-up
