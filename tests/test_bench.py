@@ -85,3 +85,22 @@ def test_gemm2_unit_figures_and_roofline_bound():
     r = bench.roofline_block("gemm2", "k", 2.0, f, b, bench.PEAK_BF16_TFLOPS, "none")
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s"
     assert abs(r["frac"] - f / 2e-3 / 1e12 / 2500.0) < 1e-9
+
+
+def test_committed_profiles_name_the_kernels_bench_reports():
+    """profiles/kernel_avg_us.json (the rocprofv3 trace of this bench) has an entry for the kernel
+    family bench.py names for each GEMM of each default workload, so every roofline block carries
+    its rocprof figure; a changed kernel-family threshold without retaken profiles fails here."""
+    import json
+    from justgoal_amd import inputs as jin
+    with open(os.path.join(ROOT, "profiles", "kernel_avg_us.json")) as f:
+        prof = json.load(f)["workloads"]
+    for name in bench.DEFAULT_WORKLOADS:
+        cfg = jin.CONFIGS[name]
+        for kernel in (bench.gemm1_kernel_name(cfg), bench.gemm2_kernel_name(cfg)):
+            assert kernel in prof[name], (name, kernel, sorted(prof[name]))
+            assert bench.load_rocprof_avg_us(kernel, name) == prof[name][kernel]["average_us"] > 0
+    r = bench.roofline_block("gemm1_swiglu", bench.gemm1_kernel_name(jin.CONFIGS["ds_t64"]), 0.075,
+                             1.0, 470e6, bench.PEAK_FP8_TFLOPS, "ds_t64")
+    us = prof["ds_t64"][r["kernel"]]["average_us"]
+    assert abs(r["frac_rocprof"] - 470e6 / (us * 1e-6) / 1e9 / bench.PEAK_HBM_GBS) < 1e-9
